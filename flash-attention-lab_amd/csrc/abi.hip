@@ -1,0 +1,266 @@
+// The C ABI declared in include/flash_lab_hip.h: argument checks, parameter derivation and
+// kernel launch. Host code only (the kernels live in prefill_fwd.hip, decode.hip, smoke.hip).
+//
+// The checks restate the reference's op-boundary checks (csrc/common/attn_host.h:18-50,
+// csrc/decode/decode_host.h:18-53, csrc/decode/decode.cu:286-293) on plain pointers and strides;
+// messages keep the reference's wording where its tests match on it.
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <string>
+
+#include "flash_lab_hip.h"
+#include "launch.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& message) {
+  g_last_error = message;
+  return code;
+}
+
+std::string fmt(const char* f, long long a) {
+  char buf[256];
+  std::snprintf(buf, sizeof(buf), f, a);
+  return buf;
+}
+
+bool aligned(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+// A kernel that moves 16 bytes at a time needs every row to start on a 16-byte boundary: the data
+// pointer is 16-byte aligned and every outer stride (of a dimension longer than 1) is a multiple
+// of 16 bytes.
+bool rows_16_byte(const void* p, int elem_bytes, int64_t size0, int64_t stride0, int64_t size1,
+                  int64_t stride1, int64_t size2, int64_t stride2) {
+  const int64_t elems = 16 / elem_bytes;
+  return aligned(p, 16) && (size0 == 1 || stride0 % elems == 0) &&
+         (size1 == 1 || stride1 % elems == 0) && (size2 == 1 || stride2 % elems == 0);
+}
+
+int elem_bytes(int32_t dtype) { return dtype == FL_DTYPE_F32 ? 4 : 2; }
+
+bool valid_scale(double s) { return std::isfinite(s) && s > 0.0; }
+
+// Decode workgroups per CU that the split heuristic aims for (FLASH_LAB_DECODE_WG_PER_CU
+// overrides it for experiments).
+int decode_target_wg_per_cu() {
+  if (const char* env = std::getenv("FLASH_LAB_DECODE_WG_PER_CU")) {
+    const int v = std::atoi(env);
+    if (v >= 1 && v <= 64) return v;
+  }
+  return 4;
+}
+
+// Smallest power of two that gives about decode_target_wg_per_cu() workgroups per CU while each
+// split of the longest possible sequence keeps at least 256 keys.
+int choose_num_splits(int64_t workgroups, int max_seqlen, int cu_count) {
+  const int64_t target = static_cast<int64_t>(decode_target_wg_per_cu()) * (cu_count > 0 ? cu_count : 256);
+  int n = 1;
+  while (n < 128 && workgroups * n < target && max_seqlen / (2 * n) >= 256) n *= 2;
+  return n;
+}
+
+int check_decode_shape(const fl_decode_params* p) {
+  if (p == nullptr) return fail(FL_ERR_INVALID, "null decode parameters");
+  if (p->dtype != FL_DTYPE_BF16 && p->dtype != FL_DTYPE_F16 && p->dtype != FL_DTYPE_F32)
+    return fail(FL_ERR_UNSUPPORTED, "decode takes bf16, fp16, or fp32");
+  if (p->head_dim != 64 && p->head_dim != 128)
+    return fail(FL_ERR_UNSUPPORTED, fmt("unsupported head_dim %lld", p->head_dim));
+  if (p->batch <= 0 || p->heads <= 0 || p->heads_kv <= 0 || p->max_seqlen <= 0)
+    return fail(FL_ERR_INVALID, "empty input");
+  if (p->heads % p->heads_kv != 0)
+    return fail(FL_ERR_INVALID, "query heads must be a multiple of KV heads");
+  return FL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fl_last_error(void) { return g_last_error.c_str(); }
+
+const char* fl_version(void) { return "flash_lab_hip 0.1.0 gfx950"; }
+
+int fl_attention_fwd(const fl_attn_params* p, fl_stream_t stream) {
+  if (p == nullptr) return fail(FL_ERR_INVALID, "null attention parameters");
+  if (p->dtype != FL_DTYPE_BF16 && p->dtype != FL_DTYPE_F16)
+    return fail(FL_ERR_UNSUPPORTED, "attention_mma_pipelined takes bf16 or fp16");
+  if (p->head_dim != 64 && p->head_dim != 128)
+    return fail(FL_ERR_UNSUPPORTED, fmt("unsupported head_dim %lld", p->head_dim));
+  if (p->batch <= 0 || p->seqlen_q <= 0 || p->seqlen_k <= 0 || p->heads <= 0 || p->heads_kv <= 0)
+    return fail(FL_ERR_INVALID, "empty input");
+  if (p->heads % p->heads_kv != 0)
+    return fail(FL_ERR_INVALID, "query heads must be a multiple of KV heads");
+  if (!valid_scale(p->softmax_scale)) return fail(FL_ERR_INVALID, "softmax_scale must be positive");
+  if (!p->q || !p->k || !p->v || !p->o || !p->lse)
+    return fail(FL_ERR_INVALID, "null tensor pointer");
+  const int eb = elem_bytes(p->dtype);
+  if (!rows_16_byte(p->q, eb, p->batch, p->q_batch_stride, p->seqlen_q, p->q_seq_stride, p->heads,
+                    p->q_head_stride))
+    return fail(FL_ERR_INVALID, "q must have 16-byte aligned rows (data pointer and strides)");
+  if (!rows_16_byte(p->k, eb, p->batch, p->k_batch_stride, p->seqlen_k, p->k_seq_stride,
+                    p->heads_kv, p->k_head_stride))
+    return fail(FL_ERR_INVALID, "k must have 16-byte aligned rows (data pointer and strides)");
+  if (!rows_16_byte(p->v, eb, p->batch, p->v_batch_stride, p->seqlen_k, p->v_seq_stride,
+                    p->heads_kv, p->v_head_stride))
+    return fail(FL_ERR_INVALID, "v must have 16-byte aligned rows (data pointer and strides)");
+  if (!rows_16_byte(p->o, eb, p->batch, p->o_batch_stride, p->seqlen_q, p->o_seq_stride, p->heads,
+                    p->o_head_stride))
+    return fail(FL_ERR_INVALID, "o must have 16-byte aligned rows (data pointer and strides)");
+  if (!aligned(p->lse, 4)) return fail(FL_ERR_INVALID, "lse must be 4-byte aligned");
+
+  const int64_t q_blocks = (static_cast<int64_t>(p->seqlen_q) + fl::kPrefillBlockM - 1) /
+                           fl::kPrefillBlockM;
+  const int64_t blocks = q_blocks * p->batch * p->heads;
+  if (blocks > (int64_t{1} << 24))
+    return fail(FL_ERR_INVALID, "batch * heads * query blocks exceeds the grid limit");
+
+  fl::PrefillArgs a{};
+  a.q = static_cast<const uint16_t*>(p->q);
+  a.k = static_cast<const uint16_t*>(p->k);
+  a.v = static_cast<const uint16_t*>(p->v);
+  a.o = static_cast<uint16_t*>(p->o);
+  a.lse = p->lse;
+  a.q_bs = p->q_batch_stride;
+  a.q_ss = p->q_seq_stride;
+  a.q_hs = p->q_head_stride;
+  a.k_bs = p->k_batch_stride;
+  a.k_ss = p->k_seq_stride;
+  a.k_hs = p->k_head_stride;
+  a.v_bs = p->v_batch_stride;
+  a.v_ss = p->v_seq_stride;
+  a.v_hs = p->v_head_stride;
+  a.o_bs = p->o_batch_stride;
+  a.o_ss = p->o_seq_stride;
+  a.o_hs = p->o_head_stride;
+  a.batch = p->batch;
+  a.seqlen_q = p->seqlen_q;
+  a.seqlen_k = p->seqlen_k;
+  a.heads = p->heads;
+  a.heads_kv = p->heads_kv;
+  a.group = p->heads / p->heads_kv;
+  a.causal_offset = p->seqlen_k - p->seqlen_q;
+  a.causal = p->causal != 0;
+  a.scale = static_cast<float>(p->softmax_scale);
+  a.scale_log2 = static_cast<float>(p->softmax_scale * 1.4426950408889634);
+  a.q_blocks = static_cast<int>(q_blocks);
+
+  const fl::DType dt = p->dtype == FL_DTYPE_BF16 ? fl::DType::bf16 : fl::DType::f16;
+  const hipError_t err = fl::launch_prefill(a, dt, p->head_dim, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(FL_ERR_LAUNCH, std::string("prefill launch: ") + hipGetErrorString(err));
+  return FL_OK;
+}
+
+int fl_decode_plan(const fl_decode_params* p, int32_t requested_splits, int32_t allow_splits,
+                   int32_t cu_count, int32_t* num_splits, size_t* workspace_bytes) {
+  if (int rc = check_decode_shape(p)) return rc;
+  if (requested_splits < 0 || requested_splits > 128)
+    return fail(FL_ERR_INVALID, "num_splits must be in [0, 128]");
+  if (num_splits == nullptr || workspace_bytes == nullptr)
+    return fail(FL_ERR_INVALID, "null output pointer");
+  const int group = p->heads / p->heads_kv;
+  const int head_chunks = group / fl::decode_heads_per_workgroup(group);
+  const int64_t workgroups = static_cast<int64_t>(p->batch) * p->heads_kv * head_chunks;
+  int n = 1;
+  if (allow_splits) {
+    n = requested_splits > 0 ? requested_splits
+                             : choose_num_splits(workgroups, p->max_seqlen, cu_count);
+  }
+  *num_splits = n;
+  *workspace_bytes =
+      n > 1 ? static_cast<size_t>(p->batch) * p->heads * n * (p->head_dim + 2) * sizeof(float) : 0;
+  return FL_OK;
+}
+
+int fl_decode(const fl_decode_params* p, fl_stream_t stream) {
+  if (int rc = check_decode_shape(p)) return rc;
+  if (!p->q || !p->k_cache || !p->v_cache || !p->o || !p->lse || !p->seq_lens)
+    return fail(FL_ERR_INVALID, "null tensor pointer");
+  if (!valid_scale(p->softmax_scale)) return fail(FL_ERR_INVALID, "softmax_scale must be positive");
+  if (p->num_splits < 1 || p->num_splits > 128)
+    return fail(FL_ERR_INVALID, "num_splits must be in [1, 128]");
+  const int eb = elem_bytes(p->dtype);
+  if (!rows_16_byte(p->q, eb, p->batch, p->q_batch_stride, p->heads, p->q_head_stride, 1, 0))
+    return fail(FL_ERR_INVALID, "q must have 16-byte aligned rows");
+  if (!rows_16_byte(p->k_cache, eb, p->batch, p->k_batch_stride, p->max_seqlen, p->k_seq_stride,
+                    p->heads_kv, p->k_head_stride))
+    return fail(FL_ERR_INVALID, "k_cache must have 16-byte aligned rows (data pointer and strides)");
+  if (!rows_16_byte(p->v_cache, eb, p->batch, p->v_batch_stride, p->max_seqlen, p->v_seq_stride,
+                    p->heads_kv, p->v_head_stride))
+    return fail(FL_ERR_INVALID, "v_cache must have 16-byte aligned rows (data pointer and strides)");
+  if (!aligned(p->o, eb) || !aligned(p->lse, 4) || !aligned(p->seq_lens, 4))
+    return fail(FL_ERR_INVALID, "o, lse and seq_lens must be aligned to their element size");
+
+  const int group = p->heads / p->heads_kv;
+  const int head_chunks = group / fl::decode_heads_per_workgroup(group);
+  const int64_t blocks = static_cast<int64_t>(p->batch) * p->heads_kv * head_chunks * p->num_splits;
+  if (blocks > (int64_t{1} << 24) || static_cast<int64_t>(p->batch) * p->heads > (int64_t{1} << 24))
+    return fail(FL_ERR_INVALID, "batch * heads too large");
+
+  fl::DecodeArgs a{};
+  a.q = p->q;
+  a.k = p->k_cache;
+  a.v = p->v_cache;
+  a.o = p->o;
+  a.lse = p->lse;
+  a.seq_lens = p->seq_lens;
+  a.q_bs = p->q_batch_stride;
+  a.q_hs = p->q_head_stride;
+  a.k_bs = p->k_batch_stride;
+  a.k_ss = p->k_seq_stride;
+  a.k_hs = p->k_head_stride;
+  a.v_bs = p->v_batch_stride;
+  a.v_ss = p->v_seq_stride;
+  a.v_hs = p->v_head_stride;
+  a.o_bs = p->o_batch_stride;
+  a.o_hs = p->o_head_stride;
+  a.batch = p->batch;
+  a.heads = p->heads;
+  a.heads_kv = p->heads_kv;
+  a.group = group;
+  a.max_seqlen = p->max_seqlen;
+  a.num_splits = p->num_splits;
+  a.head_chunks = head_chunks;
+  a.scale_log2 = static_cast<float>(p->softmax_scale * 1.4426950408889634);
+  if (p->num_splits > 1) {
+    const size_t need =
+        static_cast<size_t>(p->batch) * p->heads * p->num_splits * (p->head_dim + 2) * sizeof(float);
+    if (p->workspace == nullptr || p->workspace_bytes < need || !aligned(p->workspace, 4))
+      return fail(FL_ERR_INVALID, "decode workspace is missing or smaller than fl_decode_plan reports");
+    a.partial_o = p->workspace;
+    a.partial_ml =
+        p->workspace + static_cast<size_t>(p->batch) * p->heads * p->num_splits * p->head_dim;
+  }
+  const fl::DType dt = p->dtype == FL_DTYPE_BF16 ? fl::DType::bf16
+                       : p->dtype == FL_DTYPE_F16 ? fl::DType::f16
+                                                  : fl::DType::f32;
+  const hipError_t err = fl::launch_decode(a, dt, p->head_dim, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(FL_ERR_LAUNCH, std::string("decode launch: ") + hipGetErrorString(err));
+  return FL_OK;
+}
+
+int fl_smoke_axpy(const float* x, const float* y, float alpha, float* out, int64_t n,
+                  fl_stream_t stream) {
+  if (n < 0) return fail(FL_ERR_INVALID, "n must be non-negative");
+  if (n > 0 && (!x || !y || !out)) return fail(FL_ERR_INVALID, "null tensor pointer");
+  if (n > (int64_t{1} << 40)) return fail(FL_ERR_INVALID, "n too large");
+  const hipError_t err = fl::launch_axpy(x, y, alpha, out, n, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(FL_ERR_LAUNCH, std::string("axpy launch: ") + hipGetErrorString(err));
+  return FL_OK;
+}
+
+int fl_mfma_tile_test(const void* a, const void* b, float* c, int32_t k, int32_t trans_b,
+                      fl_stream_t stream) {
+  if (k != 16 && k != 32 && k != 64) return fail(FL_ERR_INVALID, "a must be [16, K] with K in {16, 32, 64}");
+  if (!a || !b || !c) return fail(FL_ERR_INVALID, "null tensor pointer");
+  const hipError_t err =
+      fl::launch_mfma_tile_test(static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), c,
+                                k, trans_b != 0, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(FL_ERR_LAUNCH, std::string("tile test launch: ") + hipGetErrorString(err));
+  return FL_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,97 @@
+"""Builds the gfx950 C-ABI library, flash_lab/libflash_lab_hip.so, with hipcc.
+
+    python flash-attention-lab_amd/csrc/build.py [-v]
+
+Each .hip file is compiled to an object in csrc/_build (in parallel), then linked into one shared
+library next to the Python package, which loads it with ctypes. No CMake, no torch extension
+machinery: the library has a plain C ABI (include/flash_lab_hip.h).
+"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+CSRC = Path(__file__).resolve().parent
+PKG_ROOT = CSRC.parent
+REPO = PKG_ROOT.parent
+INCLUDE = REPO / "include"
+BUILD_DIR = CSRC / "_build"
+OUTPUT = PKG_ROOT / "flash_lab" / "libflash_lab_hip.so"
+
+SOURCES = ("abi.hip", "prefill_fwd.hip", "decode.hip", "smoke.hip")
+ARCH = "gfx950"
+FLAGS = (
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    # Packed fp32 VALU forms are kept out of the device code on purpose.
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+)
+
+
+def hipcc() -> str:
+    found = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(found).exists():
+        raise RuntimeError("hipcc not found (is ROCm installed under /opt/rocm?)")
+    return found
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the device-only feature; that is expected.
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compiles every source and links OUTPUT; always rebuilds. Returns the library path."""
+    compiler = hipcc()
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    includes = [f"-I{INCLUDE}", f"-I{CSRC}"]
+    objects = []
+    commands = []
+    for src in SOURCES:
+        obj = BUILD_DIR / (Path(src).stem + ".o")
+        objects.append(obj)
+        commands.append([compiler, *FLAGS, *includes, "-c", str(CSRC / src), "-o", str(obj)])
+    workers = jobs or min(len(commands), os.cpu_count() or 1)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
+        for fut in [pool.submit(_run, cmd, verbose) for cmd in commands]:
+            fut.result()
+    tmp = OUTPUT.with_suffix(".so.tmp")
+    _run([compiler, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)],
+         verbose)
+    os.replace(tmp, OUTPUT)
+    return OUTPUT
+
+
+def main(argv=None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("-v", "--verbose", action="store_true")
+    parser.add_argument("-j", "--jobs", type=int)
+    args = parser.parse_args(argv)
+    path = build(verbose=args.verbose, jobs=args.jobs)
+    print(f"built {path}")
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,308 @@
+// Split-KV decode for gfx950: one query token per sequence against its first seq_lens[b] cached
+// keys, read in place from a [B, S_max, H_kv, D] cache through strides.
+//
+// Serves the decode_splitkv and decode_inplace ops of the reference (csrc/decode/decode.cu:40-347).
+// The arithmetic follows the reference's definitions (q pre-scaled into the log2 domain,
+// exp2 online softmax, fixed-order log-sum-exp merge of the splits, decode.cu:67-75, 116-133,
+// 204-228); the decomposition is this file's own:
+//
+//  * A workgroup (4 waves) serves one KV head and all the query heads of its group that it is
+//    given (kHeads of them), over one contiguous key range (its split). Every K and V row it reads
+//    serves all kHeads heads.
+//  * A cache row (D elements) is read as 16-byte pieces by a group of D * elem / 16 lanes, so
+//    every load instruction moves whole rows. Each lane keeps, per head, the running max and sum of
+//    its group's keys and the output columns of its own piece; no lane ever needs another lane's
+//    V data, and the only cross-lane step in the loop is the dot-product reduction of the group.
+//  * Each lane has kUnroll rows of K and of V in flight per iteration (non-temporal loads: the
+//    cache is read once).
+//  * At the end the row groups are merged by a fixed butterfly inside each wave, then the four
+//    waves in order through LDS. With one split the workgroup writes o and lse; otherwise it
+//    writes its unnormalized partial output and (max, sum), and decode_merge_kernel combines the
+//    splits in index order. No atomics: results are bitwise reproducible for a given split count.
+#include "gfx950.hpp"
+#include "launch.hpp"
+
+namespace fl {
+namespace decode {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kUnroll = 4;
+constexpr float kLn2 = 0.693147180559945309f;
+
+// Elements of a 16-byte piece as floats.
+template <typename Tag>
+__device__ __forceinline__ void unpack(const u32x4& w, float (&x)[16 / sizeof(typename Elem<Tag>::storage)]) {
+  if constexpr (sizeof(typename Elem<Tag>::storage) == 4) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = __uint_as_float(w[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = Elem<Tag>::to_float(static_cast<uint16_t>(w[e] & 0xffffu));
+      x[2 * e + 1] = Elem<Tag>::to_float(static_cast<uint16_t>(w[e] >> 16));
+    }
+  }
+}
+
+template <typename Tag, int D, int kHeads>
+__global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeArgs a) {
+  using S = typename Elem<Tag>::storage;
+  constexpr int kEPL = 16 / static_cast<int>(sizeof(S));  // elements per 16-byte piece
+  constexpr int kLPR = D / kEPL;                           // lanes per cache row
+  constexpr int kGPW = 64 / kLPR;                          // row groups per wave
+  constexpr int kGroups = kWaves * kGPW;                   // row groups per workgroup
+  constexpr int kKeysPerIter = kGroups * kUnroll;
+  static_assert(kLPR >= 1 && kLPR <= 64 && 64 % kLPR == 0, "row pieces must tile a wave");
+
+  __shared__ float red_o[kWaves][kHeads][D];
+  __shared__ float red_m[kWaves][kHeads];
+  __shared__ float red_l[kWaves][kHeads];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int piece = lane % kLPR;                   // which 16-byte piece of a row
+  const int group = wave * kGPW + lane / kLPR;     // row group within the workgroup
+
+  int w = blockIdx.x;
+  const int split = w % a.num_splits;
+  w /= a.num_splits;
+  const int hchunk = w % a.head_chunks;
+  w /= a.head_chunks;
+  const int hkv = w % a.heads_kv;
+  const int b = w / a.heads_kv;
+  const int h0 = hkv * a.group + hchunk * kHeads;
+
+  // Lengths are not checked on the host (that would need a sync); clamp them to the cache so an
+  // out-of-range value cannot read outside it.
+  const int len = min(max(a.seq_lens[b], 0), a.max_seqlen);
+  const int per_split =
+      ((len + a.num_splits - 1) / a.num_splits + kKeysPerIter - 1) / kKeysPerIter * kKeysPerIter;
+  const int k_begin = split * per_split;
+  const int k_end = min(len, k_begin + per_split);
+
+  float q[kHeads][kEPL];
+#pragma unroll
+  for (int g = 0; g < kHeads; ++g) {
+    const S* qrow = static_cast<const S*>(a.q) + b * a.q_bs + (h0 + g) * a.q_hs;
+    unpack<Tag>(load16(qrow + piece * kEPL), q[g]);
+#pragma unroll
+    for (int e = 0; e < kEPL; ++e) q[g][e] *= a.scale_log2;
+  }
+
+  float o[kHeads][kEPL];
+  float m[kHeads];  // running max, log2 units (same on every lane of a row group)
+  float l[kHeads];  // running sum (same on every lane of a row group)
+#pragma unroll
+  for (int g = 0; g < kHeads; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < kEPL; ++e) o[g][e] = 0.f;
+  }
+
+  const S* kbase = static_cast<const S*>(a.k) + b * a.k_bs + hkv * a.k_hs + piece * kEPL;
+  const S* vbase = static_cast<const S*>(a.v) + b * a.v_bs + hkv * a.v_hs + piece * kEPL;
+
+  for (int base = k_begin; base < k_end; base += kKeysPerIter) {
+    u32x4 kr[kUnroll];
+    u32x4 vr[kUnroll];
+    bool valid[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int key = base + u * kGroups + group;
+      valid[u] = key < k_end;
+      if (valid[u]) {
+        kr[u] = load16_stream(kbase + static_cast<int64_t>(key) * a.k_ss);
+        vr[u] = load16_stream(vbase + static_cast<int64_t>(key) * a.v_ss);
+      } else {
+        kr[u] = u32x4{0, 0, 0, 0};
+        vr[u] = u32x4{0, 0, 0, 0};
+      }
+    }
+    float kf[kUnroll][kEPL];
+    float vf[kUnroll][kEPL];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      unpack<Tag>(kr[u], kf[u]);
+      unpack<Tag>(vr[u], vf[u]);
+    }
+#pragma unroll
+    for (int g = 0; g < kHeads; ++g) {
+      float s[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        float dot = 0.f;
+#pragma unroll
+        for (int e = 0; e < kEPL; ++e) dot = fmaf(q[g][e], kf[u][e], dot);
+#pragma unroll
+        for (int off = 1; off < kLPR; off <<= 1) dot += __shfl_xor(dot, off);
+        s[u] = valid[u] ? dot : -INFINITY;
+      }
+      float mx = s[0];
+#pragma unroll
+      for (int u = 1; u < kUnroll; ++u) mx = fmaxf(mx, s[u]);
+      const float m_new = fmaxf(m[g], mx);
+      const float ref = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2_fast(m[g] - ref);
+      m[g] = m_new;
+      float lsum = l[g] * alpha;
+#pragma unroll
+      for (int e = 0; e < kEPL; ++e) o[g][e] *= alpha;
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const float p = exp2_fast(s[u] - ref);
+        lsum += p;
+#pragma unroll
+        for (int e = 0; e < kEPL; ++e) o[g][e] = fmaf(p, vf[u][e], o[g][e]);
+      }
+      l[g] = lsum;
+    }
+  }
+
+  // Merge the row groups of this wave: butterfly over lanes with the same piece.
+#pragma unroll
+  for (int mask = kLPR; mask < 64; mask <<= 1) {
+#pragma unroll
+    for (int g = 0; g < kHeads; ++g) {
+      const float m_o = __shfl_xor(m[g], mask);
+      const float l_o = __shfl_xor(l[g], mask);
+      const float m_new = fmaxf(m[g], m_o);
+      // Groups without keys (m = -inf) contribute nothing; two empty groups stay empty.
+      const float f = m[g] == -INFINITY ? 0.f : exp2_fast(m[g] - m_new);
+      const float f_o = m_o == -INFINITY ? 0.f : exp2_fast(m_o - m_new);
+      l[g] = l[g] * f + l_o * f_o;
+#pragma unroll
+      for (int e = 0; e < kEPL; ++e) {
+        const float o_o = __shfl_xor(o[g][e], mask);
+        o[g][e] = o[g][e] * f + o_o * f_o;
+      }
+      m[g] = m_new;
+    }
+  }
+  if (lane < kLPR) {
+#pragma unroll
+    for (int g = 0; g < kHeads; ++g) {
+#pragma unroll
+      for (int e = 0; e < kEPL; ++e) red_o[wave][g][piece * kEPL + e] = o[g][e];
+      if (lane == 0) {
+        red_m[wave][g] = m[g];
+        red_l[wave][g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+
+  // Merge the four waves in order and write o/lse (one split) or the partials.
+  for (int idx = tid; idx < kHeads * D; idx += kThreads) {
+    const int g = idx / D;
+    const int d = idx - g * D;
+    float mm = -INFINITY;
+#pragma unroll
+    for (int wv = 0; wv < kWaves; ++wv) mm = fmaxf(mm, red_m[wv][g]);
+    float num = 0.f;
+    float den = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < kWaves; ++wv) {
+      const float mw = red_m[wv][g];
+      if (mw != -INFINITY) {
+        const float f = exp2_fast(mw - mm);
+        num += red_o[wv][g][d] * f;
+        den += red_l[wv][g] * f;
+      }
+    }
+    const int h = h0 + g;
+    if (a.num_splits == 1) {
+      S* orow = static_cast<S*>(a.o) + b * a.o_bs + h * a.o_hs;
+      orow[d] = Elem<Tag>::from_float(den > 0.f ? num / den : 0.f);
+      if (d == 0) a.lse[b * a.heads + h] = den > 0.f ? mm * kLn2 + logf(den) : -INFINITY;
+    } else {
+      const int64_t slot = (static_cast<int64_t>(b) * a.heads + h) * a.num_splits + split;
+      a.partial_o[slot * D + d] = num;
+      if (d == 0) {
+        a.partial_ml[2 * slot] = mm;
+        a.partial_ml[2 * slot + 1] = den;
+      }
+    }
+  }
+}
+
+// Combines the splits of one (sequence, head) in index order: m = max_s m_s,
+// l = sum_s l_s 2^(m_s - m), o = sum_s o_s 2^(m_s - m) / l, lse = m ln 2 + ln l.
+// One workgroup of D threads per (sequence, head); empty splits (m_s = -inf) are skipped.
+template <typename Tag, int D>
+__global__ void __launch_bounds__(D) decode_merge_kernel(const DecodeArgs a) {
+  using S = typename Elem<Tag>::storage;
+  const int bh = blockIdx.x;
+  const int d = threadIdx.x;
+  const int n = a.num_splits;
+  const float* ml = a.partial_ml + static_cast<int64_t>(bh) * n * 2;
+  const float* po = a.partial_o + static_cast<int64_t>(bh) * n * D;
+  float mm = -INFINITY;
+  for (int s = 0; s < n; ++s) mm = fmaxf(mm, ml[2 * s]);
+  float num = 0.f;
+  float den = 0.f;
+  for (int s = 0; s < n; ++s) {
+    const float ms = ml[2 * s];
+    if (ms != -INFINITY) {
+      const float f = exp2_fast(ms - mm);
+      num += po[s * D + d] * f;
+      den += ml[2 * s + 1] * f;
+    }
+  }
+  const int b = bh / a.heads;
+  const int h = bh - b * a.heads;
+  S* orow = static_cast<S*>(a.o) + b * a.o_bs + h * a.o_hs;
+  orow[d] = Elem<Tag>::from_float(den > 0.f ? num / den : 0.f);
+  if (d == 0) a.lse[bh] = den > 0.f ? mm * kLn2 + logf(den) : -INFINITY;
+}
+
+template <typename Tag, int D, int kHeads>
+hipError_t launch_heads(const DecodeArgs& args, hipStream_t stream) {
+  const int blocks = args.batch * args.heads_kv * args.head_chunks * args.num_splits;
+  hipLaunchKernelGGL((decode_split_kernel<Tag, D, kHeads>), dim3(blocks), dim3(kThreads), 0, stream,
+                     args);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || args.num_splits == 1) return err;
+  hipLaunchKernelGGL((decode_merge_kernel<Tag, D>), dim3(args.batch * args.heads), dim3(D), 0,
+                     stream, args);
+  return hipGetLastError();
+}
+
+template <typename Tag, int D>
+hipError_t launch_dim(const DecodeArgs& args, int k_heads, hipStream_t stream) {
+  switch (k_heads) {
+    case 1: return launch_heads<Tag, D, 1>(args, stream);
+    case 2: return launch_heads<Tag, D, 2>(args, stream);
+    case 4: return launch_heads<Tag, D, 4>(args, stream);
+    default: return launch_heads<Tag, D, 8>(args, stream);
+  }
+}
+
+template <typename Tag>
+hipError_t launch_type(const DecodeArgs& args, int head_dim, int k_heads, hipStream_t stream) {
+  return head_dim == 64 ? launch_dim<Tag, 64>(args, k_heads, stream)
+                        : launch_dim<Tag, 128>(args, k_heads, stream);
+}
+
+}  // namespace
+}  // namespace decode
+
+int decode_heads_per_workgroup(int group) {
+  int k = 1;
+  while (k < 8 && group % (2 * k) == 0) k *= 2;
+  return k;
+}
+
+hipError_t launch_decode(const DecodeArgs& args, DType dtype, int head_dim, hipStream_t stream) {
+  const int k_heads = args.group / args.head_chunks;
+  switch (dtype) {
+    case DType::bf16: return decode::launch_type<bf16_tag>(args, head_dim, k_heads, stream);
+    case DType::f16: return decode::launch_type<f16_tag>(args, head_dim, k_heads, stream);
+    default: return decode::launch_type<f32_tag>(args, head_dim, k_heads, stream);
+  }
+}
+
+}  // namespace fl

@@ -1,0 +1,65 @@
+// Internal interface between the C ABI (abi.cpp) and the kernel files. Device-side argument
+// structs are passed to the kernels by value; everything in them is already validated.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fl {
+
+// Prefill problem as the kernels see it. Tensors are [B, S, H, D] with unit stride in D; strides
+// are in elements. Query head h reads KV head h / group; query row i sees key j iff
+// j <= i + causal_offset (bottom-right aligned causal mask).
+struct PrefillArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  float* lse;  // [B, H, S_q]
+  int64_t q_bs, q_ss, q_hs;
+  int64_t k_bs, k_ss, k_hs;
+  int64_t v_bs, v_ss, v_hs;
+  int64_t o_bs, o_ss, o_hs;
+  int batch, seqlen_q, seqlen_k, heads, heads_kv, group, causal_offset, causal;
+  float scale;       // softmax scale, natural-log domain (used for the LSE)
+  float scale_log2;  // scale * log2(e): probabilities are 2^(s * scale_log2 - ref)
+  int q_blocks;      // ceil(S_q / rows per workgroup)
+};
+
+// Decode problem. q [B, H, D], caches [B, S_max, H_kv, D], o [B, H, D], lse [B, H].
+struct DecodeArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;
+  const int32_t* seq_lens;
+  int64_t q_bs, q_hs;
+  int64_t k_bs, k_ss, k_hs;
+  int64_t v_bs, v_ss, v_hs;
+  int64_t o_bs, o_hs;
+  int batch, heads, heads_kv, group, max_seqlen;
+  int num_splits;
+  int head_chunks;   // group / heads served per workgroup
+  float scale_log2;  // q is multiplied by this, so scores are in the log2 domain
+  float* partial_o;  // [B, H, num_splits, D] unnormalized fp32 partial outputs
+  float* partial_ml; // [B, H, num_splits, 2] (max in log2 units, sum) per split
+};
+
+enum class DType : int { bf16 = 0, f16 = 1, f32 = 2 };
+
+// Rows of queries per prefill workgroup (the kernel's tile height).
+constexpr int kPrefillBlockM = 128;
+
+hipError_t launch_prefill(const PrefillArgs& args, DType dtype, int head_dim, hipStream_t stream);
+
+// Query heads one decode workgroup serves for a GQA group size (a power of two dividing it).
+int decode_heads_per_workgroup(int group);
+hipError_t launch_decode(const DecodeArgs& args, DType dtype, int head_dim, hipStream_t stream);
+
+hipError_t launch_axpy(const float* x, const float* y, float alpha, float* out, int64_t n,
+                       hipStream_t stream);
+hipError_t launch_mfma_tile_test(const uint16_t* a, const uint16_t* b, float* c, int k,
+                                 int trans_b, hipStream_t stream);
+
+}  // namespace fl

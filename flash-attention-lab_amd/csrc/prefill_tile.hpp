@@ -1,0 +1,72 @@
+// Fragment-level pieces of the prefill kernel, shared with the MFMA tile test so the lane
+// layouts are checked in isolation.
+//
+// Each wave owns 32 query rows. Scores are computed transposed, S^T = K Q^T, on
+// v_mfma_f32_32x32x16: K (keys x dims) is the A operand read from LDS, Q^T the B operand held in
+// registers for the whole kernel. In the accumulator layout lane l then holds query row l % 32
+// and 16 of the 32 keys of a key block, the other 16 being in lane l ^ 32; a row's max and sum
+// need one exchange between the two halves of the wave and no other cross-lane traffic.
+//
+// The output is accumulated transposed too, O^T = V^T P^T, so lane l keeps query row l % 32 and
+// the per-row rescale is a per-lane multiply. P^T is the B operand: lane l must supply 8 keys of
+// its own row, and it supplies exactly the ones it holds. For key step kk (16 keys) the B
+// operand's k index 8 * half + 4 * a + b (half = l / 32) is key 16 * kk + 8 * a + 4 * half + b,
+// which are accumulator registers 8 * (kk % 2) + 0..7 of key block kk / 2. V^T, the A operand,
+// is read with that same key order: two ds_read_b64_tr_b16 per operand, each returning 4
+// consecutive keys of one column.
+#pragma once
+
+#include "gfx950.hpp"
+
+namespace fl::prefill {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kRowsPerWave = 32;
+constexpr int kBlockM = kRowsPerWave * kWaves;  // query rows per workgroup
+constexpr int kBlockN = 64;                     // keys per tile
+
+// LDS row pitch in elements: rows are padded by 16 bytes.
+template <int D>
+constexpr int kPitch = D + 8;
+template <int D>
+constexpr int kTileElems = kBlockN * kPitch<D>;
+
+// A operand of S^T += K Q^T for key block mb (32 keys) and dim step ks (16 dims):
+// lane l reads K[32 mb + l % 32][16 ks + 8 (l / 32) .. + 7], one 16-byte LDS read.
+template <int D>
+__device__ __forceinline__ u32x4 k_frag(const uint16_t* k_tile, int mb, int ks, int lane) {
+  const uint16_t* p = k_tile + (32 * mb + (lane & 31)) * kPitch<D> + 16 * ks + 8 * (lane >> 5);
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+// A operand of O^T += V^T P^T for dim block nb (32 dims) and key step kk (16 keys): lane l needs
+// V[16 kk + 4 half + e][32 nb + l % 32] for e = 0..3, then the same 8 keys further on. Within
+// each 16-lane group, lane i addresses row i / 4 and columns 4 (i % 4) .. + 3 of the 4 x 16 block,
+// so that the transpose read hands lane i column i of all 4 rows.
+template <int D>
+__device__ __forceinline__ u32x4 v_frag(const uint16_t* v_tile, int nb, int kk, int lane) {
+  const int i = lane & 15;
+  const uint16_t* p = v_tile + (16 * kk + 4 * (lane >> 5) + (i >> 2)) * kPitch<D> + 32 * nb +
+                      16 * ((lane >> 4) & 1) + 4 * (i & 3);
+  const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr16(p));
+  const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr16(p + 8 * kPitch<D>));
+  return u32x4{lo.x, lo.y, hi.x, hi.y};
+}
+
+// B operand of O^T += V^T P^T for key step kk from the probabilities of key block kk / 2:
+// registers 8 * (kk % 2) .. + 7, rounded to the input type.
+template <typename Tag, int kHalf>
+__device__ __forceinline__ u32x4 p_frag(const f32x16& s) {
+  using E = Elem<Tag>;
+  constexpr int j = 8 * kHalf;
+  return u32x4{E::pack2(s[j], s[j + 1]), E::pack2(s[j + 2], s[j + 3]), E::pack2(s[j + 4], s[j + 5]),
+               E::pack2(s[j + 6], s[j + 7])};
+}
+
+// Key offset within a 32-key block of accumulator register j in a lane of the given half.
+__device__ __forceinline__ constexpr int acc_key(int j, int half) {
+  return 8 * (j >> 2) + 4 * half + (j & 3);
+}
+
+}  // namespace fl::prefill

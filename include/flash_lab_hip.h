@@ -1,0 +1,144 @@
+/*
+ * flash_lab_hip.h — C ABI of the gfx950 (MI355X) attention kernels.
+ *
+ * This library replaces the reference's op registry and host wrappers
+ * (reference csrc/bindings.cpp:7-42 plus the TORCH_LIBRARY_IMPL blocks of
+ * csrc/prefill/mma_pipelined.cu:162-189, csrc/decode/decode.cu:282-347,
+ * csrc/common/smoke.cu:29-45 and csrc/prefill/mma_tile_test.cu:62-88).
+ * The functions take plain pointers, element strides and sizes; no torch
+ * types cross this boundary. The caller owns every buffer: inputs are
+ * borrowed, outputs and the decode workspace are allocated by the caller
+ * (the Python layer allocates them through the torch caching allocator, so
+ * the calls are safe under stream capture). Nothing here allocates device
+ * memory or synchronizes; every kernel is launched on the given stream.
+ *
+ * Return value: 0 on success, otherwise an FL_ERR_* code; fl_last_error()
+ * then returns a message for the calling thread.
+ */
+#ifndef FLASH_LAB_HIP_H
+#define FLASH_LAB_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* A hipStream_t. NULL is the null stream of the current device. */
+typedef void* fl_stream_t;
+
+enum fl_dtype { FL_DTYPE_BF16 = 0, FL_DTYPE_F16 = 1, FL_DTYPE_F32 = 2 };
+
+enum fl_status {
+  FL_OK = 0,
+  FL_ERR_INVALID = 1,     /* bad argument: shape, stride, alignment, dtype */
+  FL_ERR_UNSUPPORTED = 2, /* valid, but no kernel is built for it (head_dim, dtype) */
+  FL_ERR_LAUNCH = 3       /* the HIP runtime reported an error at launch */
+};
+
+/*
+ * Prefill (attention forward). Replaces AttnParams (reference
+ * csrc/common/params.h:9-27) as filled by make_attn_params
+ * (csrc/common/attn_host.h:59-93). q is [B, S_q, H, D]; k and v are
+ * [B, S_k, H_kv, D]; o is [B, S_q, H, D] in the input dtype; lse is
+ * [B, H, S_q] fp32, contiguous. Strides are in elements; D has unit stride.
+ * The library derives group = H / H_kv, causal_offset = S_k - S_q and
+ * scale * log2(e) (computed in double, as the reference does).
+ */
+typedef struct fl_attn_params {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;
+  int64_t q_batch_stride, q_seq_stride, q_head_stride;
+  int64_t k_batch_stride, k_seq_stride, k_head_stride;
+  int64_t v_batch_stride, v_seq_stride, v_head_stride;
+  int64_t o_batch_stride, o_seq_stride, o_head_stride;
+  int32_t batch, seqlen_q, seqlen_k, heads, heads_kv, head_dim;
+  int32_t causal; /* nonzero: bottom-right aligned causal mask */
+  int32_t dtype;  /* enum fl_dtype: BF16 or F16 */
+  double softmax_scale;
+} fl_attn_params;
+
+/*
+ * FlashAttention-2 forward on MFMA. Serves the attention_mma_pipelined and
+ * attention_mma ops (reference csrc/prefill/mma_pipelined.cu:162-183,
+ * csrc/prefill/mma.cu), head_dim 64 or 128, bf16 or fp16.
+ */
+int fl_attention_fwd(const fl_attn_params* p, fl_stream_t stream);
+
+/*
+ * Decode. Replaces DecodeParams (reference csrc/common/params.h:31-53) as
+ * filled by make_decode_params (csrc/decode/decode_host.h:55-85). q is
+ * [B, H, D]; caches are [B, S_max, H_kv, D] read in place through strides;
+ * seq_lens [B] int32 on the device (never read by the host); o [B, H, D] in
+ * the input dtype; lse [B, H] fp32 contiguous. num_splits must be resolved
+ * by fl_decode_plan first. workspace is fp32 device memory of at least the
+ * size fl_decode_plan reports (unused, may be NULL, when num_splits == 1).
+ */
+typedef struct fl_decode_params {
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  void* o;
+  float* lse;
+  const int32_t* seq_lens;
+  int64_t q_batch_stride, q_head_stride;
+  int64_t k_batch_stride, k_seq_stride, k_head_stride;
+  int64_t v_batch_stride, v_seq_stride, v_head_stride;
+  int64_t o_batch_stride, o_head_stride;
+  int32_t batch, heads, heads_kv, head_dim, max_seqlen;
+  int32_t num_splits; /* >= 1 */
+  int32_t dtype;      /* enum fl_dtype: BF16, F16 or F32 */
+  double softmax_scale;
+  float* workspace;
+  size_t workspace_bytes;
+} fl_decode_params;
+
+/*
+ * Split count and workspace size for a decode call; host-only, touches no
+ * device. Replaces choose_num_splits and the workspace sizing of run_decode
+ * (reference csrc/decode/decode.cu:272-311). requested_splits 0 lets the
+ * library choose from cu_count (allow_splits != 0) or forces 1
+ * (allow_splits == 0, the decode_inplace op). Requested counts must be in
+ * [0, 128].
+ */
+int fl_decode_plan(const fl_decode_params* p, int32_t requested_splits, int32_t allow_splits,
+                   int32_t cu_count, int32_t* num_splits, size_t* workspace_bytes);
+
+/*
+ * Split-KV decode: partial passes over contiguous key ranges with fp32
+ * partials, then a fixed-order log-sum-exp merge (reference
+ * csrc/decode/decode.cu:40-235). With num_splits == 1 the single pass
+ * writes o and lse directly (the decode_inplace op).
+ */
+int fl_decode(const fl_decode_params* p, fl_stream_t stream);
+
+/* out = alpha * x + y over n fp32 elements (reference csrc/common/smoke.cu:12-45). */
+int fl_smoke_axpy(const float* x, const float* y, float alpha, float* out, int64_t n,
+                  fl_stream_t stream);
+
+/*
+ * One wave computes a 16 x 16 fp32 tile through the same fragment code as
+ * the prefill kernel (reference csrc/prefill/mma_tile_test.cu:20-84).
+ * a is [16, k] bf16 row-major, k in {16, 32, 64}. trans_b == 0: b is
+ * [16, k] and c = a b^T (b read like K in Q K^T). trans_b != 0: b is [k, 16]
+ * and c = a b (b read like V in P V, through the LDS transpose read).
+ * c is [16, 16] fp32 row-major.
+ */
+int fl_mfma_tile_test(const void* a, const void* b, float* c, int32_t k, int32_t trans_b,
+                      fl_stream_t stream);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* fl_last_error(void);
+
+/* Library version string, for environment records. */
+const char* fl_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASH_LAB_HIP_H */

@@ -1,0 +1,138 @@
+"""The C ABI boundary on the CPU: the library loads, exports every function the header declares,
+plans decode splits on the host, and rejects bad arguments before any launch. No compute call
+reaches a device here."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from flash_lab import _hip
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "flash_lab_hip.h"
+
+
+def declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^\s*(?:int|const char\*)\s+(fl_\w+)\s*\(", text, flags=re.M))
+
+
+def test_header_declares_the_abi():
+    assert declared_functions() >= {
+        "fl_attention_fwd",
+        "fl_decode_plan",
+        "fl_decode",
+        "fl_smoke_axpy",
+        "fl_mfma_tile_test",
+        "fl_last_error",
+        "fl_version",
+    }
+
+
+def test_library_exports_every_declared_function():
+    lib = ctypes.CDLL(str(_hip.LIB_PATH))
+    for name in sorted(declared_functions()):
+        assert hasattr(lib, name), name
+    assert set(_hip.SIGNATURES) == declared_functions()
+
+
+def test_struct_layouts_match_the_header():
+    # Natural C alignment: 5 pointers + 12 int64 + 8 int32 + double = 176 bytes;
+    # 6 pointers + 10 int64 + 7 int32 (+4 pad) + double + pointer + size_t = 184 bytes.
+    assert ctypes.sizeof(_hip.AttnParams) == 176
+    assert ctypes.sizeof(_hip.DecodeParams) == 184
+    assert _hip.AttnParams.softmax_scale.offset == 168
+    assert _hip.DecodeParams.softmax_scale.offset == 160
+
+
+def test_version():
+    assert b"gfx950" in _hip.LIB.fl_version()
+
+
+@pytest.mark.parametrize(
+    "batch,heads,heads_kv,expected_splits",
+    [(1, 32, 32, 32), (8, 32, 32, 4), (8, 32, 8, 16)],
+    ids=["B1-MHA", "B8-MHA", "B8-GQA"],
+)
+def test_decode_plan_on_256_cus(batch, heads, heads_kv, expected_splits):
+    splits, ws = _hip.decode_plan(batch, heads, heads_kv, 128, 32768, torch.bfloat16)
+    assert splits == expected_splits
+    assert ws == batch * heads * splits * (128 + 2) * 4
+
+
+def test_decode_plan_requested_and_inplace():
+    assert _hip.decode_plan(2, 8, 8, 64, 1000, torch.float16, num_splits=7) == (7, 2 * 8 * 7 * 66 * 4)
+    # decode_inplace: one split and no workspace whatever is asked.
+    assert _hip.decode_plan(2, 8, 8, 64, 1000, torch.float16, num_splits=7, allow_splits=False) == (
+        1,
+        0,
+    )
+    # Short caches keep >= 256 keys per split.
+    assert _hip.decode_plan(1, 8, 8, 128, 500, torch.bfloat16)[0] == 1
+    assert _hip.decode_plan(1, 8, 8, 128, 512, torch.bfloat16)[0] == 2
+
+
+def test_decode_plan_rejections():
+    with pytest.raises(RuntimeError, match=r"num_splits must be in \[0, 128\]"):
+        _hip.decode_plan(1, 8, 8, 128, 100, torch.bfloat16, num_splits=129)
+    with pytest.raises(RuntimeError, match="unsupported head_dim 96"):
+        _hip.decode_plan(1, 8, 8, 96, 100, torch.bfloat16)
+    with pytest.raises(RuntimeError, match="multiple of KV heads"):
+        _hip.decode_plan(1, 6, 4, 128, 100, torch.bfloat16)
+
+
+def _attn_params(**over):
+    p = _hip.AttnParams()
+    p.q = p.k = p.v = p.o = p.lse = 256
+    p.batch, p.seqlen_q, p.seqlen_k, p.heads, p.heads_kv, p.head_dim = 1, 8, 8, 2, 2, 128
+    p.q_batch_stride = p.k_batch_stride = p.v_batch_stride = p.o_batch_stride = 8 * 2 * 128
+    p.q_seq_stride = p.k_seq_stride = p.v_seq_stride = p.o_seq_stride = 2 * 128
+    p.q_head_stride = p.k_head_stride = p.v_head_stride = p.o_head_stride = 128
+    p.dtype = 0
+    p.softmax_scale = 0.125
+    for key, value in over.items():
+        setattr(p, key, value)
+    return p
+
+
+@pytest.mark.parametrize(
+    "over,message",
+    [
+        ({"dtype": 2}, "takes bf16 or fp16"),
+        ({"head_dim": 96}, "unsupported head_dim 96"),
+        ({"heads_kv": 3}, "multiple of KV heads"),
+        ({"seqlen_k": 0}, "empty input"),
+        ({"softmax_scale": -1.0}, "softmax_scale must be positive"),
+        ({"q": 258}, "q must have 16-byte aligned rows"),
+        ({"k_seq_stride": 2 * 128 + 4}, "k must have 16-byte aligned rows"),
+        ({"q": 0}, "null tensor pointer"),
+    ],
+)
+def test_attention_rejects_before_launch(over, message):
+    rc = _hip.LIB.fl_attention_fwd(ctypes.byref(_attn_params(**over)), None)
+    assert rc != 0
+    assert message in _hip.LIB.fl_last_error().decode()
+
+
+def test_decode_rejects_missing_workspace():
+    p = _hip.DecodeParams()
+    p.q = p.k_cache = p.v_cache = p.o = p.lse = p.seq_lens = 256
+    p.batch, p.heads, p.heads_kv, p.head_dim, p.max_seqlen = 1, 8, 8, 128, 1000
+    p.q_batch_stride, p.q_head_stride = 8 * 128, 128
+    p.k_batch_stride = p.v_batch_stride = 1000 * 8 * 128
+    p.k_seq_stride = p.v_seq_stride = 8 * 128
+    p.k_head_stride = p.v_head_stride = 128
+    p.o_batch_stride, p.o_head_stride = 8 * 128, 128
+    p.dtype, p.softmax_scale, p.num_splits = 0, 0.1, 4
+    assert _hip.LIB.fl_decode(ctypes.byref(p), None) != 0
+    assert "workspace" in _hip.LIB.fl_last_error().decode()
+    p.num_splits = 0
+    assert _hip.LIB.fl_decode(ctypes.byref(p), None) != 0
+    assert "num_splits must be in [1, 128]" in _hip.LIB.fl_last_error().decode()
+
+
+def test_tile_test_rejects_bad_k():
+    assert _hip.LIB.fl_mfma_tile_test(256, 256, 256, 48, 0, None) != 0
+    assert "K in {16, 32, 64}" in _hip.LIB.fl_last_error().decode()

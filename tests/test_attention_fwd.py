@@ -1,0 +1,150 @@
+"""Prefill kernel parity against the fp64 oracle, under the reference's tolerance rule.
+
+Shape list, edge cases and rule follow the reference's tests/test_attention_fwd.py:18-177: ragged
+lengths, S_q != S_k both ways (causal rows without keys), GQA, packed strided inputs, scores of
+order 100, bitwise determinism, rejection of unsupported inputs. Added here: the headline shape
+(4, 32, 32, 4096, 128) checked on sampled rows, and the two tensor-core impl names serving the same
+kernel.
+"""
+
+import pytest
+import torch
+
+import flash_lab
+from parity import check_prefill
+
+pytestmark = pytest.mark.gpu
+
+IMPLS = [
+    ("mma_pipelined", torch.bfloat16),
+    ("mma_pipelined", torch.float16),
+]
+
+SHAPES = [
+    # batch, seqlen_q, seqlen_k, heads, heads_kv, head_dim
+    (1, 1, 1, 1, 1, 64),
+    (3, 7, 7, 8, 8, 64),
+    (1, 16, 16, 1, 1, 128),
+    (3, 63, 63, 8, 2, 128),
+    (1, 128, 128, 8, 1, 64),
+    (3, 257, 257, 8, 8, 128),
+    (1, 1024, 1024, 8, 2, 64),
+    (2, 1024, 1024, 4, 4, 128),
+    (2, 37, 101, 4, 2, 64),  # S_q < S_k
+    (1, 101, 37, 4, 4, 128),  # S_q > S_k: causal rows without keys
+    (2, 1, 300, 8, 2, 128),
+]
+SLOW_SHAPES = [(1, 4096, 4096, 4, 4, 128), (1, 8192, 8192, 2, 1, 64)]
+
+
+def make_inputs(shape, dtype, scale=1.0):
+    batch, seqlen_q, seqlen_k, heads, heads_kv, head_dim = shape
+    q = torch.randn(batch, seqlen_q, heads, head_dim, device="cuda", dtype=dtype) * scale
+    k = torch.randn(batch, seqlen_k, heads_kv, head_dim, device="cuda", dtype=dtype) * scale
+    v = torch.randn(batch, seqlen_k, heads_kv, head_dim, device="cuda", dtype=dtype)
+    return q, k, v
+
+
+def sampled_rows(seqlen, count, seed=0):
+    """First, last and a seeded sample of the rows in between (the reference's bench/run.py)."""
+    if seqlen <= count:
+        return torch.arange(seqlen)
+    gen = torch.Generator().manual_seed(seed)
+    middle = torch.randperm(seqlen - 2, generator=gen)[: count - 2] + 1
+    return torch.cat([torch.tensor([0, seqlen - 1]), middle]).sort().values
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("shape", SHAPES, ids=str)
+@pytest.mark.parametrize("impl,dtype", IMPLS, ids=lambda x: str(x).replace("torch.", ""))
+def test_matches_reference(impl, dtype, shape, causal):
+    print(f"prefill {impl} {dtype} {shape} causal={causal}", flush=True)
+    q, k, v = make_inputs(shape, dtype)
+    out, lse = flash_lab.attention(q, k, v, causal=causal, impl=impl, return_lse=True)
+    check_prefill(out, lse, q, k, v, causal)
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("shape", SLOW_SHAPES, ids=str)
+def test_long_sequences(shape, causal):
+    q, k, v = make_inputs(shape, torch.bfloat16)
+    out, lse = flash_lab.attention(q, k, v, causal=causal, return_lse=True)
+    check_prefill(out, lse, q, k, v, causal, rows=sampled_rows(shape[1], 256))
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_headline_shape_sampled_rows(causal):
+    # (B, H, H_kv, S, D) = (4, 32, 32, 4096, 128) bf16, seeded like the benchmark (q, k, v order).
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    shape = (4, 4096, 32, 128)
+    q, k, v = (torch.randn(shape, device="cuda", dtype=torch.bfloat16, generator=gen) for _ in range(3))
+    out, lse = flash_lab.attention(q, k, v, causal=causal, return_lse=True)
+    check_prefill(out, lse, q, k, v, causal, rows=sampled_rows(4096, 64))
+
+
+@pytest.mark.parametrize("impl,dtype", IMPLS, ids=lambda x: str(x).replace("torch.", ""))
+def test_large_scores(impl, dtype):
+    # Scores of order 100 overflow exp() unless the running max is subtracted.
+    q, k, v = make_inputs((2, 129, 129, 4, 2, 64), dtype, scale=10.0)
+    out, lse = flash_lab.attention(q, k, v, causal=True, impl=impl, return_lse=True)
+    check_prefill(out, lse, q, k, v, causal=True)
+
+
+@pytest.mark.parametrize("impl,dtype", IMPLS, ids=lambda x: str(x).replace("torch.", ""))
+def test_strided_inputs(impl, dtype):
+    # q, k, v sliced out of one packed [B, S, 3, H, D] projection: no copies, unusual strides.
+    qkv = torch.randn(2, 77, 3, 4, 64, device="cuda", dtype=dtype)
+    q, k, v = qkv.unbind(dim=2)
+    assert not q.is_contiguous()
+    out, lse = flash_lab.attention(q, k, v, causal=True, impl=impl, return_lse=True)
+    check_prefill(out, lse, q, k, v, causal=True)
+
+
+@pytest.mark.parametrize("scale", [0.05, 0.5])
+def test_explicit_softmax_scale(scale):
+    q, k, v = make_inputs((2, 70, 90, 4, 2, 128), torch.bfloat16)
+    out, lse = flash_lab.attention(q, k, v, causal=True, softmax_scale=scale, return_lse=True)
+    check_prefill(out, lse, q, k, v, causal=True, scale=scale)
+
+
+@pytest.mark.parametrize("impl,dtype", IMPLS, ids=lambda x: str(x).replace("torch.", ""))
+def test_deterministic(impl, dtype):
+    q, k, v = make_inputs((2, 300, 300, 8, 2, 128), dtype)
+    first = flash_lab.attention(q, k, v, causal=True, impl=impl)
+    second = flash_lab.attention(q, k, v, causal=True, impl=impl)
+    assert torch.equal(first, second)
+
+
+@pytest.mark.parametrize("impl,dtype", IMPLS, ids=lambda x: str(x).replace("torch.", ""))
+def test_rejects_unsupported_inputs(impl, dtype):
+    q, k, v = make_inputs((1, 8, 8, 2, 2, 96), dtype)
+    with pytest.raises(ValueError, match="head_dim"):
+        flash_lab.attention(q, k, v, impl=impl)
+    q, k, v = make_inputs((1, 8, 8, 2, 2, 64), torch.float64)
+    with pytest.raises(ValueError, match="dtype"):
+        flash_lab.attention(q, k, v, impl=impl)
+
+
+def test_both_tensor_core_names_run_the_same_kernel():
+    q, k, v = make_inputs((2, 100, 100, 4, 2, 128), torch.bfloat16)
+    a = flash_lab.attention(q, k, v, causal=True, impl="mma_pipelined")
+    b = flash_lab.attention(q, k, v, causal=True, impl="mma")
+    assert torch.equal(a, b)
+
+
+def test_auto_picks_the_hip_kernel():
+    q, k, v = make_inputs((1, 64, 64, 2, 2, 64), torch.bfloat16)
+    torch.testing.assert_close(
+        flash_lab.attention(q, k, v), flash_lab.attention(q, k, v, impl="mma_pipelined"),
+        rtol=0, atol=0,
+    )
+
+
+def test_reference_kernels_this_build_does_not_ship():
+    q, k, v = make_inputs((1, 32, 32, 2, 2, 64), torch.bfloat16)
+    with pytest.raises(RuntimeError, match="not available in this build"):
+        flash_lab.attention(q, k, v, impl="triton")
+    q32, k32, v32 = (x.float() for x in (q, k, v))
+    with pytest.raises(ValueError, match="no available implementation"):
+        flash_lab.attention(q32, k32, v32)

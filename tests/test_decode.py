@@ -1,0 +1,160 @@
+"""Decode kernel parity against the fp64 oracle, under the reference's tolerance rule.
+
+Cases follow the reference's tests/test_decode.py:11-119: three dtypes, GQA groups 1 to 8 (and a
+group of 3), ragged and random lengths, split counts with empty splits, a strided cache carved out
+of a larger allocation, rank-3 queries, bitwise determinism, rejections. Added: the three
+benchmark shapes at 32K keys, split-count invariance within tolerance, and lengths outside the
+cache (clamped on the device instead of read out of bounds).
+"""
+
+import pytest
+import torch
+
+import flash_lab
+from parity import check_decode, normwise_rel
+from oracle import reference
+
+pytestmark = pytest.mark.gpu
+
+IMPLS = ["decode_inplace", "splitkv"]
+DTYPES = [torch.bfloat16, torch.float16, torch.float32]
+
+CASES = [
+    # batch, heads, heads_kv, max_seqlen, head_dim, seq_lens
+    (1, 8, 8, 64, 64, [64]),
+    (4, 8, 1, 1100, 128, [1, 5, 1023, 1100]),
+    (3, 32, 4, 4097, 128, [4097, 64, 1024]),
+    (2, 6, 2, 300, 64, [300, 17]),
+    (2, 32, 8, 700, 128, [700, 333]),
+    (16, 8, 2, 512, 64, "random"),
+]
+
+
+def make_case(case, dtype, gen):
+    batch, heads, heads_kv, max_seqlen, head_dim, lens = case
+    q = torch.randn(batch, 1, heads, head_dim, device="cuda", dtype=dtype, generator=gen)
+    shape = (batch, max_seqlen, heads_kv, head_dim)
+    k_cache = torch.randn(shape, device="cuda", dtype=dtype, generator=gen)
+    v_cache = torch.randn(shape, device="cuda", dtype=dtype, generator=gen)
+    if lens == "random":
+        seq_lens = torch.randint(1, max_seqlen + 1, (batch,), device="cuda", generator=gen)
+    else:
+        seq_lens = torch.tensor(lens, device="cuda")
+    return q, k_cache, v_cache, seq_lens.to(torch.int32)
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"B{c[0]}-H{c[1]}-Hkv{c[2]}-S{c[3]}-D{c[4]}")
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).removeprefix("torch."))
+@pytest.mark.parametrize("impl", IMPLS)
+def test_matches_reference(impl, dtype, case):
+    print(f"decode {impl} {dtype} {case}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    q, k_cache, v_cache, seq_lens = make_case(case, dtype, gen)
+    out, lse = flash_lab.decode(q, k_cache, v_cache, seq_lens, impl=impl, return_lse=True)
+    check_decode(out, lse, q, k_cache, v_cache, seq_lens)
+
+
+@pytest.mark.parametrize("num_splits", [1, 2, 8, 64, None])
+def test_splitkv_split_counts(num_splits):
+    # More splits than keys leaves some splits empty; they must not disturb the merge.
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    q, k_cache, v_cache, seq_lens = make_case(
+        (3, 16, 4, 2000, 128, [2000, 40, 777]), torch.bfloat16, gen
+    )
+    out, lse = flash_lab.decode(
+        q, k_cache, v_cache, seq_lens, impl="splitkv", num_splits=num_splits, return_lse=True
+    )
+    check_decode(out, lse, q, k_cache, v_cache, seq_lens)
+
+
+@pytest.mark.parametrize("impl", IMPLS)
+def test_strided_cache_and_rank3_query(impl):
+    # Caches carved out of a larger allocation (every other KV head), q given as [B, H, D].
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    big = torch.randn(2, 600, 8, 128, device="cuda", dtype=torch.bfloat16, generator=gen)
+    k_cache, v_cache = big[:, :, 0::2], big[:, :, 1::2]
+    q = torch.randn(2, 16, 128, device="cuda", dtype=torch.bfloat16, generator=gen)
+    seq_lens = torch.tensor([600, 123], device="cuda", dtype=torch.int32)
+    out, lse = flash_lab.decode(q, k_cache, v_cache, seq_lens, impl=impl, return_lse=True)
+    assert out.shape == q.shape
+    check_decode(out, lse, q, k_cache, v_cache, seq_lens)
+
+
+@pytest.mark.parametrize("impl", IMPLS)
+def test_deterministic(impl):
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    q, k_cache, v_cache, seq_lens = make_case(
+        (4, 32, 8, 3000, 128, [3000, 1, 2048, 999]), torch.bfloat16, gen
+    )
+    first = flash_lab.decode(q, k_cache, v_cache, seq_lens, impl=impl)
+    second = flash_lab.decode(q, k_cache, v_cache, seq_lens, impl=impl)
+    assert torch.equal(first, second)
+
+
+def test_auto_is_splitkv():
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    q, k_cache, v_cache, seq_lens = make_case((2, 8, 8, 64, 64, [64, 3]), torch.bfloat16, gen)
+    auto = flash_lab.decode(q, k_cache, v_cache, seq_lens)
+    torch.testing.assert_close(
+        auto, flash_lab.decode(q, k_cache, v_cache, seq_lens, impl="splitkv"), rtol=0, atol=0
+    )
+
+
+@pytest.mark.parametrize("impl", IMPLS)
+def test_rejects_unsupported(impl):
+    q = torch.randn(1, 1, 4, 96, device="cuda", dtype=torch.bfloat16)
+    cache = torch.randn(1, 8, 4, 96, device="cuda", dtype=torch.bfloat16)
+    seq_lens = torch.tensor([8], device="cuda", dtype=torch.int32)
+    with pytest.raises(ValueError, match="head_dim"):
+        flash_lab.decode(q, cache, cache, seq_lens, impl=impl)
+    q, cache = q[..., :64], torch.randn(4, 4, 4, 64, device="cuda", dtype=torch.bfloat16)
+    tables = torch.zeros(1, 2, device="cuda", dtype=torch.int32)
+    with pytest.raises(ValueError, match="paged"):
+        flash_lab.decode(q.contiguous(), cache, cache, seq_lens, block_tables=tables, impl=impl)
+
+
+@pytest.mark.parametrize(
+    "batch,heads_kv",
+    [(1, 32), pytest.param(8, 32, marks=pytest.mark.slow), (8, 8)],
+    ids=["B1-MHA", "B8-MHA", "B8-GQA"],
+)
+def test_benchmark_shapes_at_32k(batch, heads_kv):
+    # The three decode configurations of the benchmark: 32K valid keys in a [B, 32768, H_kv, 128]
+    # bf16 cache, seeded like the benchmark (q, k_cache, v_cache order).
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn(batch, 1, 32, 128, device="cuda", dtype=torch.bfloat16, generator=gen)
+    shape = (batch, 32768, heads_kv, 128)
+    k_cache = torch.randn(shape, device="cuda", dtype=torch.bfloat16, generator=gen)
+    v_cache = torch.randn(shape, device="cuda", dtype=torch.bfloat16, generator=gen)
+    seq_lens = torch.full((batch,), 32768, device="cuda", dtype=torch.int32)
+    out, lse = flash_lab.decode(q, k_cache, v_cache, seq_lens, return_lse=True)
+    check_decode(out, lse, q, k_cache, v_cache, seq_lens)
+
+
+def test_split_count_changes_results_only_within_tolerance():
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    q, k_cache, v_cache, seq_lens = make_case(
+        (2, 8, 2, 5000, 128, [5000, 2500]), torch.float32, gen
+    )
+    ref = reference.decode(q.cpu(), k_cache.cpu(), v_cache.cpu(), seq_lens.cpu())
+    for n in (1, 3, 16, 128):
+        out = flash_lab.decode(q, k_cache, v_cache, seq_lens, num_splits=n)
+        # fp32 path: within 1e-5 relative (normwise) of fp64 for every split count.
+        assert normwise_rel(out.cpu(), ref) <= 1e-5, n
+
+
+def test_lengths_outside_the_cache_are_clamped():
+    # seq_lens is not checked on the host; the kernel clamps it to [0, S_max] so that a bad value
+    # cannot read outside the cache. A length above S_max behaves as S_max.
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    q, k_cache, v_cache, _ = make_case((2, 4, 4, 100, 64, [100, 100]), torch.float32, gen)
+    too_long = torch.tensor([100000, 100], device="cuda", dtype=torch.int32)
+    full = torch.tensor([100, 100], device="cuda", dtype=torch.int32)
+    torch.testing.assert_close(
+        flash_lab.decode(q, k_cache, v_cache, too_long),
+        flash_lab.decode(q, k_cache, v_cache, full),
+        rtol=0, atol=0,
+    )
+    empty = torch.tensor([0, 100], device="cuda", dtype=torch.int32)
+    out, lse = flash_lab.decode(q, k_cache, v_cache, empty, return_lse=True)
+    assert torch.all(out[0] == 0) and torch.isneginf(lse[0]).all()
