@@ -300,8 +300,42 @@ def parse_args(argv=None):
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--decode-steps", type=int, default=100)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--only", choices=["prefill", "decode"])
+    parser.add_argument(
+        "--only",
+        help="comma list of workloads to run: prefill, prefill_causal, decode (all three), "
+        f"{', '.join(DECODE)}, copy (a 1 GiB device copy, the calibration of the traffic "
+        "counters); default: all but copy",
+    )
     return parser.parse_args(argv)
+
+
+def selected_workloads(only: str | None) -> list[str]:
+    everything = ["prefill", "prefill_causal", *DECODE]
+    if not only:
+        return everything
+    names = []
+    for item in only.split(","):
+        item = item.strip()
+        if item == "decode":
+            names += list(DECODE)
+        elif item in everything or item == "copy":
+            names.append(item)
+        else:
+            raise SystemExit(f"unknown workload {item!r}")
+    return names
+
+
+def bench_copy(steps: int) -> dict:
+    """A plain 1 GiB device-to-device copy: its FETCH_SIZE / WRITE_SIZE readings per dispatch
+    calibrate the traffic counters against a known byte count."""
+    import torch
+
+    src = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    times, _ = time_op(lambda: dst.copy_(src), steps, 2)
+    mean_ms = sum(times) / len(times)
+    return {"status": "ok", "bytes_read": FLUSH_BYTES, "bytes_written": FLUSH_BYTES,
+            "mean_ms": mean_ms, "gbps_read_plus_write": 2 * FLUSH_BYTES / (mean_ms / 1e3) / 1e9}
 
 
 def main(argv=None) -> int:
@@ -326,21 +360,27 @@ def main(argv=None) -> int:
         return 2
 
     props = torch.cuda.get_device_properties(0)
+    workloads = selected_workloads(args.only)
     secondary = {}
     headline = None
-    if args.only != "decode":
+    if "prefill" in workloads:
         headline = bench_prefill(args.steps, args.warmup, causal=False)
         print(f"# prefill non-causal: {json.dumps(headline)}", file=sys.stderr, flush=True)
+    if "prefill_causal" in workloads:
         secondary["prefill_causal"] = bench_prefill(args.steps, args.warmup, causal=True)
         print(f"# prefill causal: {json.dumps(secondary['prefill_causal'])}", file=sys.stderr,
               flush=True)
-    if args.only != "prefill":
+    decodes = [name for name in DECODE if name in workloads]
+    if decodes:
         flush = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda")
-        for name in DECODE:
+        for name in decodes:
             secondary[f"decode_{name}"] = bench_decode(name, args.decode_steps, 10, flush)
             print(f"# decode {name}: {json.dumps(secondary[f'decode_{name}'])}", file=sys.stderr,
                   flush=True)
         del flush
+    if "copy" in workloads:
+        secondary["copy"] = bench_copy(args.steps)
+        print(f"# copy: {json.dumps(secondary['copy'])}", file=sys.stderr, flush=True)
 
     if headline is not None and headline["status"] == "ok":
         value = headline["tflops"]

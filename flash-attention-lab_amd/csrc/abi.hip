@@ -111,6 +111,13 @@ int fl_attention_fwd(const fl_attn_params* p, fl_stream_t stream) {
                     p->o_head_stride))
     return fail(FL_ERR_INVALID, "o must have 16-byte aligned rows (data pointer and strides)");
   if (!aligned(p->lse, 4)) return fail(FL_ERR_INVALID, "lse must be 4-byte aligned");
+  // Tile loads address K and V rows through 32-bit byte offsets from a per-tile base, and rely on
+  // rows not overlapping (sequence stride >= head_dim) to zero-fill past the end.
+  const int64_t max_seq_stride = ((int64_t{1} << 31) / 2 - p->head_dim) / fl::kPrefillBlockN;
+  if (p->seqlen_k > 1 && (p->k_seq_stride < p->head_dim || p->v_seq_stride < p->head_dim))
+    return fail(FL_ERR_INVALID, "k and v rows must not overlap (sequence stride >= head_dim)");
+  if (p->k_seq_stride > max_seq_stride || p->v_seq_stride > max_seq_stride)
+    return fail(FL_ERR_INVALID, "k or v sequence stride too large");
 
   const int64_t q_blocks = (static_cast<int64_t>(p->seqlen_q) + fl::kPrefillBlockM - 1) /
                            fl::kPrefillBlockM;

@@ -61,34 +61,48 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(err, file=sys.stderr)
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compiles every source and links OUTPUT; always rebuilds. Returns the library path."""
+def build(
+    verbose: bool = False,
+    jobs: int | None = None,
+    defines: tuple[str, ...] = (),
+    output: Path | None = None,
+) -> Path:
+    """Compiles every source and links the library (OUTPUT unless `output` is given); always
+    rebuilds. `defines` are NAME=VALUE preprocessor settings of the kernels' tuning knobs."""
     compiler = hipcc()
-    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    output = Path(output) if output is not None else OUTPUT
+    build_dir = BUILD_DIR if output == OUTPUT else output.parent / f"_build_{output.stem}"
+    build_dir.mkdir(parents=True, exist_ok=True)
     includes = [f"-I{INCLUDE}", f"-I{CSRC}"]
+    macro_flags = [f"-D{d}" for d in defines]
     objects = []
     commands = []
     for src in SOURCES:
-        obj = BUILD_DIR / (Path(src).stem + ".o")
+        obj = build_dir / (Path(src).stem + ".o")
         objects.append(obj)
-        commands.append([compiler, *FLAGS, *includes, "-c", str(CSRC / src), "-o", str(obj)])
+        commands.append(
+            [compiler, *FLAGS, *macro_flags, *includes, "-c", str(CSRC / src), "-o", str(obj)]
+        )
     workers = jobs or min(len(commands), os.cpu_count() or 1)
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
         for fut in [pool.submit(_run, cmd, verbose) for cmd in commands]:
             fut.result()
-    tmp = OUTPUT.with_suffix(".so.tmp")
+    tmp = output.with_suffix(".so.tmp")
     _run([compiler, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)],
          verbose)
-    os.replace(tmp, OUTPUT)
-    return OUTPUT
+    os.replace(tmp, output)
+    return output
 
 
 def main(argv=None) -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("-v", "--verbose", action="store_true")
     parser.add_argument("-j", "--jobs", type=int)
+    parser.add_argument("-D", "--define", action="append", default=[], help="NAME=VALUE knob")
+    parser.add_argument("-o", "--output", type=Path)
     args = parser.parse_args(argv)
-    path = build(verbose=args.verbose, jobs=args.jobs)
+    path = build(verbose=args.verbose, jobs=args.jobs, defines=tuple(args.define),
+                 output=args.output)
     print(f"built {path}")
     return 0
 

@@ -28,7 +28,11 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kUnroll = 4;
+// Cache rows of K and of V each lane has in flight per iteration.
+#ifndef FL_DECODE_UNROLL
+#define FL_DECODE_UNROLL 8
+#endif
+constexpr int kUnroll = FL_DECODE_UNROLL;
 constexpr float kLn2 = 0.693147180559945309f;
 
 // Elements of a 16-byte piece as floats.
@@ -137,8 +141,7 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeArgs
         float dot = 0.f;
 #pragma unroll
         for (int e = 0; e < kEPL; ++e) dot = fmaf(q[g][e], kf[u][e], dot);
-#pragma unroll
-        for (int off = 1; off < kLPR; off <<= 1) dot += __shfl_xor(dot, off);
+        dot = group_sum<kLPR>(dot);
         s[u] = valid[u] ? dot : -INFINITY;
       }
       float mx = s[0];
@@ -241,9 +244,11 @@ __global__ void __launch_bounds__(D) decode_merge_kernel(const DecodeArgs a) {
   const float* ml = a.partial_ml + static_cast<int64_t>(bh) * n * 2;
   const float* po = a.partial_o + static_cast<int64_t>(bh) * n * D;
   float mm = -INFINITY;
+#pragma unroll 8
   for (int s = 0; s < n; ++s) mm = fmaxf(mm, ml[2 * s]);
   float num = 0.f;
   float den = 0.f;
+#pragma unroll 8
   for (int s = 0; s < n; ++s) {
     const float ms = ml[2 * s];
     if (ms != -INFINITY) {

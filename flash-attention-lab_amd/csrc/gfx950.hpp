@@ -20,6 +20,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
@@ -43,9 +46,9 @@ struct Elem<bf16_tag> {
   static __device__ __forceinline__ uint16_t from_float(float x) {
     return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
   }
-  // Two floats packed into one dword, lower address first.
+  // Two floats packed into one dword, lower address first (one v_cvt_pk_bf16_f32, RNE).
   static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    return static_cast<uint32_t>(from_float(lo)) | (static_cast<uint32_t>(from_float(hi)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
   }
   static __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
@@ -62,8 +65,9 @@ struct Elem<f16_tag> {
   static __device__ __forceinline__ uint16_t from_float(float x) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
   }
+  // One v_cvt_pk_f16_f32 (RNE).
   static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    return static_cast<uint32_t>(from_float(lo)) | (static_cast<uint32_t>(from_float(hi)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
   }
   static __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
@@ -88,6 +92,22 @@ __device__ __forceinline__ u32x4 load16_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
+// Buffer resource over `bytes` bytes from `base` (raw addressing, no stride). A buffer load whose
+// offset is at or past `bytes` returns zeros without touching memory, which is how tile loads past
+// the end of a sequence are zero-filled without branches.
+constexpr int kBufferRsrcWord3 = 0x00020000;  // gfx9-family raw buffer configuration
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferRsrcWord3);
+}
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int offset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0));
+}
+
+// True on every lane when `pred` holds on any active lane (a wave-uniform branch condition).
+__device__ __forceinline__ bool wave_any(bool pred) {
+  return __builtin_amdgcn_ballot_w64(pred) != 0;
+}
+
 // ds_read_b64_tr_b16 on an LDS address given as a generic pointer into __shared__ memory.
 __device__ __forceinline__ i16x4 lds_read_tr16(const void* p) {
   typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
@@ -95,6 +115,30 @@ __device__ __forceinline__ i16x4 lds_read_tr16(const void* p) {
 }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// DPP lane moves within rows of 16 lanes (pure VALU, no LDS traffic).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+constexpr int kDppQuadSwap1 = 0xB1;     // quad_perm [1, 0, 3, 2]: lane ^ 1
+constexpr int kDppQuadSwap2 = 0x4E;     // quad_perm [2, 3, 0, 1]: lane ^ 2
+constexpr int kDppRowHalfMirror = 0x141;  // lane i <- lane 7 - i within each 8
+constexpr int kDppRowMirror = 0x140;      // lane i <- lane 15 - i within each 16
+
+// Sum over aligned groups of kLanes lanes (4, 8, 16, 32 or 64); every lane of a group gets the
+// same bits (each step adds a pair of equal partial sums in either order).
+template <int kLanes>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(kLanes == 4 || kLanes == 8 || kLanes == 16 || kLanes == 32 || kLanes == 64, "");
+  x += dpp_move<kDppQuadSwap1>(x);
+  x += dpp_move<kDppQuadSwap2>(x);
+  if constexpr (kLanes >= 8) x += dpp_move<kDppRowHalfMirror>(x);
+  if constexpr (kLanes >= 16) x += dpp_move<kDppRowMirror>(x);
+  if constexpr (kLanes >= 32) x += __shfl_xor(x, 16);
+  if constexpr (kLanes >= 64) x += __shfl_xor(x, 32);
+  return x;
+}
 
 // Butterfly exchange with lane ^ mask through ds_bpermute (works across the 32-lane halves).
 __device__ __forceinline__ float xor_lane(float v, int mask) {

@@ -48,8 +48,9 @@ struct DecodeArgs {
 
 enum class DType : int { bf16 = 0, f16 = 1, f32 = 2 };
 
-// Rows of queries per prefill workgroup (the kernel's tile height).
+// Rows of queries per prefill workgroup (the kernel's tile height) and keys per tile.
 constexpr int kPrefillBlockM = 128;
+constexpr int kPrefillBlockN = 64;
 
 hipError_t launch_prefill(const PrefillArgs& args, DType dtype, int head_dim, hipStream_t stream);
 

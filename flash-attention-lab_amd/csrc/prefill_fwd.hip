@@ -23,6 +23,24 @@ namespace prefill {
 namespace {
 
 constexpr int kXcds = 8;
+constexpr float kLn2 = 0.693147180559945309f;
+// log2 of the largest probability the lazily moved reference point allows.
+constexpr float kRescaleSlack = 8.f;
+
+// Max of the 32 scores a lane holds, as a tree of three-input maxes.
+__device__ __forceinline__ float max_of(const f32x16& x, const f32x16& y) {
+  float t[11];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) t[i] = fmaxf(fmaxf(x[3 * i], x[3 * i + 1]), x[3 * i + 2]);
+#pragma unroll
+  for (int i = 0; i < 5; ++i) t[5 + i] = fmaxf(fmaxf(y[3 * i], y[3 * i + 1]), y[3 * i + 2]);
+  t[10] = fmaxf(x[15], y[15]);
+  const float u0 = fmaxf(fmaxf(t[0], t[1]), t[2]);
+  const float u1 = fmaxf(fmaxf(t[3], t[4]), t[5]);
+  const float u2 = fmaxf(fmaxf(t[6], t[7]), t[8]);
+  const float u3 = fmaxf(t[9], t[10]);
+  return fmaxf(fmaxf(u0, u1), fmaxf(u2, u3));
+}
 
 // Bijection on [0, n): ids dealt to XCD x (id % 8 == x) get the contiguous range
 // [x * n / 8, (x + 1) * n / 8) of work items. A ragged tail keeps its own ids.
@@ -32,8 +50,16 @@ __device__ __forceinline__ int xcd_remap(int id, int n) {
   return (id % kXcds) * per + id / kXcds;
 }
 
+// Waves per SIMD the register allocation is held to (two: one workgroup's softmax can overlap
+// another's MFMA work on the same SIMD).
+#ifndef FL_PREFILL_WAVES_PER_EU
+#define FL_PREFILL_WAVES_PER_EU 2
+#endif
+
 template <typename Tag, int D>
-__global__ void __launch_bounds__(kThreads) prefill_fwd_kernel(const PrefillArgs a) {
+__global__ void __launch_bounds__(kThreads)
+    __attribute__((amdgpu_waves_per_eu(FL_PREFILL_WAVES_PER_EU, FL_PREFILL_WAVES_PER_EU)))
+    prefill_fwd_kernel(const PrefillArgs a) {
   using E = Elem<Tag>;
   constexpr int kTile = kTileElems<D>;
   // Two slots, each K then V.
@@ -72,26 +98,36 @@ __global__ void __launch_bounds__(kThreads) prefill_fwd_kernel(const PrefillArgs
     for (int ks = 0; ks < D / 16; ++ks) qf[ks] = ok ? load16(src + 16 * ks) : u32x4{0, 0, 0, 0};
   }
 
-  // Tile staging: each thread moves kPasses 16-byte pieces of K and of V per tile.
+  // Tile staging: each thread moves kPasses 16-byte pieces of K and of V per tile. Loads go
+  // through buffer resources rebased on each tile and sized to its valid rows, so the per-thread
+  // byte offsets are fixed for the whole kernel and, the sequence stride being at least D, rows
+  // past the end of the sequence fall outside the resource and read as zeros (0 * V stays
+  // finite) with no branch.
   constexpr int kChunks = D / 8;
   constexpr int kRowsPerPass = kThreads / kChunks;
   constexpr int kPasses = kBlockN / kRowsPerPass;
   const int st_row = tid / kChunks;
   const int st_col = (tid % kChunks) * 8;
+  int k_off[kPasses];
+  int v_off[kPasses];
+#pragma unroll
+  for (int p = 0; p < kPasses; ++p) {
+    const int r = st_row + p * kRowsPerPass;
+    k_off[p] = static_cast<int>((r * a.k_ss + st_col) * 2);
+    v_off[p] = static_cast<int>((r * a.v_ss + st_col) * 2);
+  }
   u32x4 kst[kPasses];
   u32x4 vst[kPasses];
 
   auto fetch = [&](int tile) {
+    const int k0 = tile * kBlockN;
+    const int rows = min(kBlockN, a.seqlen_k - k0);
+    const auto krs = buffer_rsrc(kp + k0 * a.k_ss, static_cast<int>(((rows - 1) * a.k_ss + D) * 2));
+    const auto vrs = buffer_rsrc(vp + k0 * a.v_ss, static_cast<int>(((rows - 1) * a.v_ss + D) * 2));
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
-      const int row = tile * kBlockN + st_row + p * kRowsPerPass;
-      if (row < a.seqlen_k) {  // rows past the end are zero so that 0 * V stays finite
-        kst[p] = load16(kp + static_cast<int64_t>(row) * a.k_ss + st_col);
-        vst[p] = load16(vp + static_cast<int64_t>(row) * a.v_ss + st_col);
-      } else {
-        kst[p] = u32x4{0, 0, 0, 0};
-        vst[p] = u32x4{0, 0, 0, 0};
-      }
+      kst[p] = buffer_load16(krs, k_off[p]);
+      vst[p] = buffer_load16(vrs, v_off[p]);
     }
   };
   auto stash = [&](int slot) {
@@ -108,8 +144,8 @@ __global__ void __launch_bounds__(kThreads) prefill_fwd_kernel(const PrefillArgs
   f32x16 o[D / 32];
 #pragma unroll
   for (int nb = 0; nb < D / 32; ++nb) o[nb] = f32x16{};
-  float m = -INFINITY;  // running max of the raw scores of my_row
-  float l = 0.f;        // this lane's share of the running sum
+  float ref = -INFINITY;  // reference point of o and l, log2 units; -inf until a key is seen
+  float l = 0.f;          // this lane's share of the running sum
   const float sl2 = a.scale_log2;
   // Last key my_row may see in the whole problem.
   const int last_key = a.causal ? min(a.seqlen_k - 1, my_row + a.causal_offset) : a.seqlen_k - 1;
@@ -150,27 +186,33 @@ __global__ void __launch_bounds__(kThreads) prefill_fwd_kernel(const PrefillArgs
     }
 
     // Online softmax in the exp2 domain on raw scores: with scale > 0,
-    // max(scale * s) = scale * max(s), and p = 2^(s * scale_log2 - m * scale_log2).
-    float mx = fmaxf(s0[0], s1[0]);
-#pragma unroll
-    for (int j = 1; j < 16; ++j) mx = fmaxf(mx, fmaxf(s0[j], s1[j]));
+    // max(scale * s) = scale * max(s), and p = 2^(s * scale_log2 - ref).
+    float mx = max_of(s0, s1);
     mx = fmaxf(mx, xor_lane(mx, 32));
-    const float m_new = fmaxf(m, mx);
-    // A row that has seen only hidden keys keeps m = -inf; 0 as its reference point keeps every
-    // exponential at exactly 0 instead of nan.
-    const float ref = m_new == -INFINITY ? 0.f : m_new * sl2;
-    const float alpha = exp2_fast(fmaf(m, sl2, -ref));
-    m = m_new;
-    float rs = 0.f;
+    // The reference point `ref` (log2 units) of o and l only moves when the row max has grown by
+    // more than kRescaleSlack over it, so probabilities stay at most 2^kRescaleSlack: no overflow,
+    // and a bf16/fp16 P keeps its relative precision. Most tiles then skip the rescale of o.
+    const float cand = mx * sl2;  // -inf while the row has seen only hidden keys
+    const bool move = cand > ref + kRescaleSlack;
+    if (wave_any(move)) {
+      const float alpha = move ? exp2_fast(ref - cand) : 1.f;  // ref = -inf gives 0
+      ref = move ? cand : ref;
+      l *= alpha;
+#pragma unroll
+      for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
+    }
+    // Rows without a visible key so far have only -inf scores: any finite shift gives p = 0.
+    const float shift = ref == -INFINITY ? 0.f : ref;
+    float rs0 = 0.f;
+    float rs1 = 0.f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      s0[j] = exp2_fast(fmaf(s0[j], sl2, -ref));
-      s1[j] = exp2_fast(fmaf(s1[j], sl2, -ref));
-      rs += s0[j] + s1[j];
+      s0[j] = exp2_fast(fmaf(s0[j], sl2, -shift));
+      s1[j] = exp2_fast(fmaf(s1[j], sl2, -shift));
+      rs0 += s0[j];
+      rs1 += s1[j];
     }
-    l = fmaf(l, alpha, rs);
-#pragma unroll
-    for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
+    l += rs0 + rs1;
 
     const u32x4 p0 = p_frag<Tag, 0>(s0);
     const u32x4 p1 = p_frag<Tag, 1>(s0);
@@ -201,8 +243,9 @@ __global__ void __launch_bounds__(kThreads) prefill_fwd_kernel(const PrefillArgs
       }
     }
     if (half == 0) {
+      // l = sum 2^(s scale_log2 - ref), so ln(sum e^(s scale)) = ref ln 2 + ln l.
       a.lse[(static_cast<int64_t>(b) * a.heads + h) * a.seqlen_q + my_row] =
-          lt > 0.f ? m * a.scale + logf(lt) : -INFINITY;
+          lt > 0.f ? ref * kLn2 + logf(lt) : -INFINITY;
     }
   }
 }
@@ -274,6 +317,7 @@ hipError_t launch_typed(const PrefillArgs& args, hipStream_t stream) {
 }  // namespace prefill
 
 static_assert(kPrefillBlockM == prefill::kBlockM, "host and kernel tile heights differ");
+static_assert(kPrefillBlockN == prefill::kBlockN, "host and kernel tile widths differ");
 
 hipError_t launch_prefill(const PrefillArgs& args, DType dtype, int head_dim, hipStream_t stream) {
   using namespace prefill;

@@ -219,6 +219,12 @@ def prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, sof
     for name, x in (("q", q), ("k", k), ("v", v)):
         _require(x.stride(-1) == 1, f"{name} must be contiguous in its last dimension")
     batch, seqlen_q, heads, head_dim = q.shape
+    # The kernel needs non-overlapping K and V rows (sequence stride >= head_dim); broadcast or
+    # overlapping views, which the reference also accepts, are passed as contiguous copies.
+    if k.shape[1] > 1 and k.stride(1) < head_dim:
+        k = k.contiguous()
+    if v.shape[1] > 1 and v.stride(1) < head_dim:
+        v = v.contiguous()
     o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty((batch, heads, seqlen_q), dtype=torch.float32, device=q.device)
     p = AttnParams(
