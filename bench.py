@@ -93,6 +93,22 @@ def cpu_model() -> str:
     return "unknown"
 
 
+TRAFFIC_PROFILE = REPO / "profiles" / "prefill_fwd_4x32x32x4096x128_bf16.md"
+
+
+def profiled_traffic(path: Path = TRAFFIC_PROFILE) -> float | None:
+    """HBM bytes per launch of the prefill kernel from its committed rocprofv3 summary (FETCH_SIZE
+    and WRITE_SIZE runs scaled by a 1 GiB copy's readings); None if there is none. bench.py cannot
+    collect counters itself, so the figure comes from the profile of the same command."""
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def sampled_rows(seqlen: int, count: int, seed: int = 0):
     import torch
 
@@ -391,7 +407,8 @@ def main(argv=None) -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": headline["tflops_mean"] / PEAK_BF16_TFLOPS,
-            "traffic": None,
+            "traffic": profiled_traffic(),
+            "traffic_source": str(TRAFFIC_PROFILE.relative_to(REPO)),
             "kernel": "prefill_fwd_kernel<bf16_tag, 128>",
             "per_launch": f"{headline['flops']:.4g} FLOP (4 B H S^2 D), mean {headline['mean_ms']:.4f} ms",
         }
