@@ -1,0 +1,57 @@
+"""CPU checks of the benchmark's host logic: work models, statistics, workload selection and the
+committed traffic figure (the reference's tests/test_bench.py:1-62 covers the same models)."""
+
+import pytest
+
+import bench
+
+
+def test_attention_flops_counts_two_matmuls_and_halves_causal():
+    full = bench.attention_flops(2, 4, 128, 256, 64, causal=False)
+    assert full == 4 * 2 * 4 * 128 * 256 * 64
+    assert bench.attention_flops(2, 4, 128, 256, 64, causal=True) == full / 2
+    # The headline configuration is 2^40 FLOP non-causal.
+    assert bench.attention_flops(4, 32, 4096, 4096, 128, causal=False) == 2.0**40
+
+
+def test_decode_bytes_read_the_kv_cache_once():
+    assert bench.decode_kv_bytes(1, 32, 32768, 128, 2) == 2**29
+    assert bench.decode_kv_bytes(8, 32, 32768, 128, 2) == 2**32
+    assert bench.decode_kv_bytes(8, 8, 32768, 128, 2) == 2**30
+    # The reference's variant adds q read and o written: 536,887,296 B at B=1 MHA.
+    assert bench.decode_bytes_with_qo(1, 32, 32, 32768, 128, 2) == 536_887_296
+
+
+def test_summarize():
+    assert bench.summarize([5.0, 1.0, 3.0, 2.0, 4.0]) == {
+        "median": 3.0, "p10": 1.0, "p90": 5.0, "min": 1.0
+    }
+
+
+def test_workload_selection():
+    assert bench.selected_workloads(None) == ["prefill", "prefill_causal", *bench.DECODE]
+    assert bench.selected_workloads("decode,copy") == [*bench.DECODE, "copy"]
+    with pytest.raises(SystemExit):
+        bench.selected_workloads("nope")
+
+
+def test_sampled_rows_keep_the_ends():
+    rows = bench.sampled_rows(4096, 64)
+    assert len(rows) == 64 and rows[0] == 0 and rows[-1] == 4095
+    assert bool((rows[1:] > rows[:-1]).all())
+
+
+def test_profiled_traffic_is_parsed(tmp_path):
+    path = tmp_path / "p.md"
+    path.write_text("# x\n\ntraffic_bytes_per_launch: 123456\n")
+    assert bench.profiled_traffic(path) == 123456.0
+    assert bench.profiled_traffic(tmp_path / "missing.md") is None
+    # The committed prefill profile carries the figure, and it is close to the algorithmic
+    # minimum of q + k + v + o + lse = 514 MiB.
+    committed = bench.profiled_traffic()
+    assert committed is not None and 500 * 2**20 < committed < 600 * 2**20
+
+
+def test_more_than_one_gpu_is_refused(capsys):
+    assert bench.main(["--gpus", "2"]) == 2
+    assert "one GPU" in capsys.readouterr().err
