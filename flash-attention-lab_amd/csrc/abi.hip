@@ -187,7 +187,7 @@ int fl_decode(const fl_decode_params* p, fl_stream_t stream) {
   if (!p->q || !p->k_cache || !p->v_cache || !p->o || !p->lse || !p->seq_lens)
     return fail(FL_ERR_INVALID, "null tensor pointer");
   if (!valid_scale(p->softmax_scale)) return fail(FL_ERR_INVALID, "softmax_scale must be positive");
-  if (p->num_splits < 1 || p->num_splits > 128)
+  if (p->num_splits < 1 || p->num_splits > fl::kMaxSplits)
     return fail(FL_ERR_INVALID, "num_splits must be in [1, 128]");
   const int eb = elem_bytes(p->dtype);
   if (!rows_16_byte(p->q, eb, p->batch, p->q_batch_stride, p->heads, p->q_head_stride, 1, 0))

@@ -230,38 +230,64 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeArgs
       }
     }
   }
+
 }
 
-// Combines the splits of one (sequence, head) in index order: m = max_s m_s,
-// l = sum_s l_s 2^(m_s - m), o = sum_s o_s 2^(m_s - m) / l, lse = m ln 2 + ln l.
-// One workgroup of D threads per (sequence, head); empty splits (m_s = -inf) are skipped.
+// Combines the splits of one (sequence, head): m = max_s m_s, l = sum_s l_s 2^(m_s - m),
+// o = sum_s o_s 2^(m_s - m) / l, lse = m ln 2 + ln l; empty splits (m_s = -inf) contribute
+// nothing. One workgroup per (sequence, head): the (m, l) pairs go through LDS, wave w sums the
+// splits w, w + 4, ... (all its loads independent, so they are in flight together), and the four
+// waves' sums are added in wave order, so the result is the same on every run.
 template <typename Tag, int D>
-__global__ void __launch_bounds__(D) decode_merge_kernel(const DecodeArgs a) {
+__global__ void __launch_bounds__(kThreads) decode_merge_kernel(const DecodeArgs a) {
   using S = typename Elem<Tag>::storage;
+  constexpr int kCols = D / 64;  // output columns per lane
+  __shared__ float m_s[kMaxSplits];
+  __shared__ float l_s[kMaxSplits];
+  __shared__ float part_num[kWaves][D];
+  __shared__ float part_den[kWaves];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int bh = blockIdx.x;
-  const int d = threadIdx.x;
   const int n = a.num_splits;
   const float* ml = a.partial_ml + static_cast<int64_t>(bh) * n * 2;
   const float* po = a.partial_o + static_cast<int64_t>(bh) * n * D;
-  float mm = -INFINITY;
-#pragma unroll 8
-  for (int s = 0; s < n; ++s) mm = fmaxf(mm, ml[2 * s]);
-  float num = 0.f;
-  float den = 0.f;
-#pragma unroll 8
-  for (int s = 0; s < n; ++s) {
-    const float ms = ml[2 * s];
-    if (ms != -INFINITY) {
-      const float f = exp2_fast(ms - mm);
-      num += po[s * D + d] * f;
-      den += ml[2 * s + 1] * f;
-    }
+  for (int s = tid; s < n; s += kThreads) {
+    m_s[s] = ml[2 * s];
+    l_s[s] = ml[2 * s + 1];
   }
-  const int b = bh / a.heads;
-  const int h = bh - b * a.heads;
-  S* orow = static_cast<S*>(a.o) + b * a.o_bs + h * a.o_hs;
-  orow[d] = Elem<Tag>::from_float(den > 0.f ? num / den : 0.f);
-  if (d == 0) a.lse[bh] = den > 0.f ? mm * kLn2 + logf(den) : -INFINITY;
+  __syncthreads();
+  float mm = -INFINITY;
+  for (int s = 0; s < n; ++s) mm = fmaxf(mm, m_s[s]);
+  float num[kCols] = {};
+  float den = 0.f;
+#pragma unroll 4
+  for (int s = wave; s < n; s += kWaves) {
+    const float ms = m_s[s];
+    const float f = ms == -INFINITY ? 0.f : exp2_fast(ms - mm);
+    den += l_s[s] * f;
+#pragma unroll
+    for (int c = 0; c < kCols; ++c) num[c] += po[s * D + c * 64 + lane] * f;
+  }
+#pragma unroll
+  for (int c = 0; c < kCols; ++c) part_num[wave][c * 64 + lane] = num[c];
+  if (lane == 0) part_den[wave] = den;
+  __syncthreads();
+  if (tid < D) {
+    float total = 0.f;
+    float total_den = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      total += part_num[w][tid];
+      total_den += part_den[w];
+    }
+    const int b = bh / a.heads;
+    const int h = bh - b * a.heads;
+    S* orow = static_cast<S*>(a.o) + b * a.o_bs + h * a.o_hs;
+    orow[tid] = Elem<Tag>::from_float(total_den > 0.f ? total / total_den : 0.f);
+    if (tid == 0) a.lse[bh] = total_den > 0.f ? mm * kLn2 + logf(total_den) : -INFINITY;
+  }
 }
 
 template <typename Tag, int D, int kHeads>
@@ -271,8 +297,8 @@ hipError_t launch_heads(const DecodeArgs& args, hipStream_t stream) {
                      args);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || args.num_splits == 1) return err;
-  hipLaunchKernelGGL((decode_merge_kernel<Tag, D>), dim3(args.batch * args.heads), dim3(D), 0,
-                     stream, args);
+  hipLaunchKernelGGL((decode_merge_kernel<Tag, D>), dim3(args.batch * args.heads), dim3(kThreads),
+                     0, stream, args);
   return hipGetLastError();
 }
 

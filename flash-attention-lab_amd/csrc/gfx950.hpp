@@ -103,6 +103,14 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int 
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0));
 }
 
+// buffer_load_dwordx4 ... lds: each lane's 16 bytes go to LDS at `lds_block` + 16 * lane (the
+// block address is wave-uniform); offsets past the resource write zeros.
+__device__ __forceinline__ void buffer_load16_to_lds(__amdgpu_buffer_rsrc_t rsrc, void* lds_block,
+                                                     int offset) {
+  typedef __attribute__((address_space(3))) void lds_void;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(lds_block), 16, offset, 0, 0, 0);
+}
+
 // True on every lane when `pred` holds on any active lane (a wave-uniform branch condition).
 __device__ __forceinline__ bool wave_any(bool pred) {
   return __builtin_amdgcn_ballot_w64(pred) != 0;

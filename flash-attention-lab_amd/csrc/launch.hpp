@@ -46,6 +46,9 @@ struct DecodeArgs {
   float* partial_ml; // [B, H, num_splits, 2] (max in log2 units, sum) per split
 };
 
+// Largest split count a decode call may use.
+constexpr int kMaxSplits = 128;
+
 enum class DType : int { bf16 = 0, f16 = 1, f32 = 2 };
 
 // Rows of queries per prefill workgroup (the kernel's tile height) and keys per tile.

@@ -15,6 +15,8 @@
 //  * Work order: the 1-D grid is remapped so each XCD (workgroups are dealt round-robin over the
 //    8 XCDs) runs a contiguous range of (batch, head) pairs and their K/V stay in that XCD's L2.
 //    Within a (batch, head) the causal query blocks run heaviest first.
+#include <type_traits>
+
 #include "launch.hpp"
 #include "prefill_tile.hpp"
 
@@ -55,6 +57,31 @@ __device__ __forceinline__ int xcd_remap(int id, int n) {
 #ifndef FL_PREFILL_WAVES_PER_EU
 #define FL_PREFILL_WAVES_PER_EU 2
 #endif
+// Scheduling hints that interleave the next tile's score MFMAs with the softmax VALU work, and
+// the VALU instructions placed after each MFMA.
+#ifndef FL_PREFILL_SCHED
+#define FL_PREFILL_SCHED 0
+#endif
+// Software pipelining: the scores of tile t + 1 computed next to the softmax of tile t (costs a
+// second score buffer of 32 registers).
+#ifndef FL_PREFILL_PIPELINE
+#define FL_PREFILL_PIPELINE 0
+#endif
+// Scheduling groups that keep the K fragment reads ahead of the score MFMAs.
+#ifndef FL_PREFILL_QK_SCHED
+#define FL_PREFILL_QK_SCHED 1
+#endif
+// K fragment reads issued ahead of their MFMAs.
+#ifndef FL_PREFILL_K_AHEAD
+#define FL_PREFILL_K_AHEAD 2
+#endif
+#ifndef FL_PREFILL_VALU_PER_MFMA
+#define FL_PREFILL_VALU_PER_MFMA 8
+#endif
+// Instruction classes of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedValu = 0x002;
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
 
 template <typename Tag, int D>
 __global__ void __launch_bounds__(kThreads)
@@ -62,12 +89,14 @@ __global__ void __launch_bounds__(kThreads)
     prefill_fwd_kernel(const PrefillArgs a) {
   using E = Elem<Tag>;
   constexpr int kTile = kTileElems<D>;
-  // Two slots, each K then V.
+  // Four tile slots: K tiles in slots 0 and 1, V tiles in slots 2 and 3.
   __shared__ __attribute__((aligned(16))) uint16_t smem[4 * kTile];
+  auto k_slot = [&](int i) { return smem + i * kTile; };
+  auto v_slot = [&](int i) { return smem + (2 + i) * kTile; };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5;
 
   const int work = xcd_remap(blockIdx.x, gridDim.x);
@@ -98,47 +127,31 @@ __global__ void __launch_bounds__(kThreads)
     for (int ks = 0; ks < D / 16; ++ks) qf[ks] = ok ? load16(src + 16 * ks) : u32x4{0, 0, 0, 0};
   }
 
-  // Tile staging: each thread moves kPasses 16-byte pieces of K and of V per tile. Loads go
-  // through buffer resources rebased on each tile and sized to its valid rows, so the per-thread
-  // byte offsets are fixed for the whole kernel and, the sequence stride being at least D, rows
-  // past the end of the sequence fall outside the resource and read as zeros (0 * V stays
-  // finite) with no branch.
-  constexpr int kChunks = D / 8;
-  constexpr int kRowsPerPass = kThreads / kChunks;
-  constexpr int kPasses = kBlockN / kRowsPerPass;
-  const int st_row = tid / kChunks;
-  const int st_col = (tid % kChunks) * 8;
-  int k_off[kPasses];
-  int v_off[kPasses];
+  // Tiles go from HBM straight into LDS (buffer_load ... lds): each wave moves kDmaPerWave
+  // 1 KiB blocks of a tile; lane l's 16 bytes land at block + 16 l, so lane l fetches the
+  // logical chunk that the swizzle stores at that position. The buffer resource is rebased on
+  // each tile and sized to its valid rows: rows past the end of the sequence (the sequence stride
+  // being at least D) fall outside it and arrive as zeros, so 0 * V stays finite.
+  constexpr int kChunksPerRow = D / 8;
+  constexpr int kRowsPerBlock = 64 / kChunksPerRow;
+  constexpr int kDmaPerWave = kBlockN / kRowsPerBlock / kWaves;
+  int k_off[kDmaPerWave];
+  int v_off[kDmaPerWave];
 #pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-    const int r = st_row + p * kRowsPerPass;
-    k_off[p] = static_cast<int>((r * a.k_ss + st_col) * 2);
-    v_off[p] = static_cast<int>((r * a.v_ss + st_col) * 2);
+  for (int j = 0; j < kDmaPerWave; ++j) {
+    const int row = (wave * kDmaPerWave + j) * kRowsPerBlock + lane / kChunksPerRow;
+    const int chunk = (lane % kChunksPerRow) ^ swz<D>(row);
+    k_off[j] = static_cast<int>((row * a.k_ss + 8 * chunk) * 2);
+    v_off[j] = static_cast<int>((row * a.v_ss + 8 * chunk) * 2);
   }
-  u32x4 kst[kPasses];
-  u32x4 vst[kPasses];
-
-  auto fetch = [&](int tile) {
+  auto dma = [&](uint16_t* slot, const uint16_t* base, int64_t seq_stride, const int(&off)[kDmaPerWave],
+                 int tile) {
     const int k0 = tile * kBlockN;
     const int rows = min(kBlockN, a.seqlen_k - k0);
-    const auto krs = buffer_rsrc(kp + k0 * a.k_ss, static_cast<int>(((rows - 1) * a.k_ss + D) * 2));
-    const auto vrs = buffer_rsrc(vp + k0 * a.v_ss, static_cast<int>(((rows - 1) * a.v_ss + D) * 2));
+    const auto rsrc = buffer_rsrc(base + k0 * seq_stride, static_cast<int>(((rows - 1) * seq_stride + D) * 2));
 #pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
-      kst[p] = buffer_load16(krs, k_off[p]);
-      vst[p] = buffer_load16(vrs, v_off[p]);
-    }
-  };
-  auto stash = [&](int slot) {
-    uint16_t* kt = smem + 2 * slot * kTile;
-    uint16_t* vt = kt + kTile;
-#pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
-      const int r = st_row + p * kRowsPerPass;
-      *reinterpret_cast<u32x4*>(kt + r * kPitch<D> + st_col) = kst[p];
-      *reinterpret_cast<u32x4*>(vt + r * kPitch<D> + st_col) = vst[p];
-    }
+    for (int j = 0; j < kDmaPerWave; ++j)
+      buffer_load16_to_lds(rsrc, slot + (wave * kDmaPerWave + j) * 512, off[j]);
   };
 
   f32x16 o[D / 32];
@@ -150,81 +163,165 @@ __global__ void __launch_bounds__(kThreads)
   // Last key my_row may see in the whole problem.
   const int last_key = a.causal ? min(a.seqlen_k - 1, my_row + a.causal_offset) : a.seqlen_k - 1;
 
-  if (num_tiles > 0) fetch(0);
-  for (int t = 0; t < num_tiles; ++t) {
-    const int slot = t & 1;
-    stash(slot);
+  // S^T of the tile in k_tile for this wave's 32 rows. K fragments are read kKAhead steps ahead
+  // of the MFMAs that consume them, so the LDS latency overlaps the MFMA chain.
+  auto scores = [&](const uint16_t* k_tile, f32x16 (&s)[2]) {
+    constexpr int kSteps = D / 16;
+    constexpr int kAhead = FL_PREFILL_K_AHEAD < kSteps ? FL_PREFILL_K_AHEAD : kSteps;
+    u32x4 a0[kSteps];
+    u32x4 a1[kSteps];
+#pragma unroll
+    for (int ks = 0; ks < kAhead; ++ks) {
+      a0[ks] = k_frag<D>(k_tile, 0, ks, lane);
+      a1[ks] = k_frag<D>(k_tile, 1, ks, lane);
+    }
+    s[0] = f32x16{};
+    s[1] = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < kSteps; ++ks) {
+      if (ks + kAhead < kSteps) {
+        a0[ks + kAhead] = k_frag<D>(k_tile, 0, ks + kAhead, lane);
+        a1[ks + kAhead] = k_frag<D>(k_tile, 1, ks + kAhead, lane);
+      }
+      s[0] = E::mfma32(a0[ks], qf[ks], s[0]);
+      s[1] = E::mfma32(a1[ks], qf[ks], s[1]);
+    }
+#if FL_PREFILL_QK_SCHED
+    // Keep the reads kAhead steps ahead: the scheduler otherwise pulls each read down to its
+    // MFMA and the LDS latency is exposed on every step.
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kAhead, 1);
+#pragma unroll
+    for (int ks = 0; ks < kSteps - kAhead; ++ks) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * kAhead, 1);
+#endif
+  };
+
+  // Prologue: K and V of tile 0 and K of tile 1 in flight (then, pipelined, the scores of tile 0).
+  f32x16 s_cur[2];
+  if (num_tiles > 0) {
+    dma(k_slot(0), kp, a.k_ss, k_off, 0);
+    dma(v_slot(0), vp, a.v_ss, v_off, 0);
+#if FL_PREFILL_PIPELINE
+    if (num_tiles > 1) dma(k_slot(1), kp, a.k_ss, k_off, 1);
+#endif
     __syncthreads();
-    if (t + 1 < num_tiles) fetch(t + 1);
+#if FL_PREFILL_PIPELINE
+    scores(k_slot(0), s_cur);
+#endif
+  }
+
+  // Iteration t: scores, softmax and P V of tile t while the next tile's loads are in flight; each
+  // load goes to the slot of tile t - 1, which every wave finished with before the last barrier.
+  // Pipelined, the scores of tile t + 1 (MFMA) are computed in the same straight-line block as the
+  // softmax of tile t (VALU) so the two interleave; K then runs two tiles ahead: K(t + 2) goes to
+  // K(t)'s slot, whose scores were computed in the previous iteration.
+  for (int t = 0; t < num_tiles; ++t) {
+#if FL_PREFILL_PIPELINE
+    if (t + 2 < num_tiles) dma(k_slot(t & 1), kp, a.k_ss, k_off, t + 2);
+#else
+    if (t + 1 < num_tiles) dma(k_slot((t + 1) & 1), kp, a.k_ss, k_off, t + 1);
+#endif
+    if (t + 1 < num_tiles) dma(v_slot((t + 1) & 1), vp, a.v_ss, v_off, t + 1);
 
     const int k0 = t * kBlockN;
-    // Every key of this tile is hidden from every row of this wave (wave-uniform).
-    if (a.causal && k0 > row0 + kRowsPerWave - 1 + a.causal_offset) continue;
-    const uint16_t* kt = smem + 2 * slot * kTile;
-    const uint16_t* vt = kt + kTile;
-
-    f32x16 s0 = f32x16{};
-    f32x16 s1 = f32x16{};
+    // A wave that sees no key of this tile sees none of the later ones either (causal).
+    const bool active = !(a.causal && k0 > row0 + kRowsPerWave - 1 + a.causal_offset);
+    if (active) {
+#if FL_PREFILL_PIPELINE
+      f32x16 s_next[2];
+#endif
+      u32x4 pf[4];
+      bool move;
+      float alpha;
+      auto step = [&](auto masked) {
+#if FL_PREFILL_PIPELINE
+        // Scores of tile t + 1. On the last tile the slot holds stale data; the result is unused.
+        scores(k_slot((t + 1) & 1), s_next);
+#else
+        scores(k_slot(t & 1), s_cur);
+#endif
+        if constexpr (decltype(masked)::value) {
+          const int lim = last_key - k0;
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
-      const u32x4 a0 = k_frag<D>(kt, 0, ks, lane);
-      const u32x4 a1 = k_frag<D>(kt, 1, ks, lane);
-      s0 = E::mfma32(a0, qf[ks], s0);
-      s1 = E::mfma32(a1, qf[ks], s1);
-    }
-
-    const bool need_mask = (k0 + kBlockN > a.seqlen_k) ||
-                           (a.causal && k0 + kBlockN - 1 > row0 + a.causal_offset);
-    if (need_mask) {
-      const int lim = last_key - k0;
+          for (int j = 0; j < 16; ++j) {
+            const int kj = acc_key(j, half);
+            if (kj > lim) s_cur[0][j] = -INFINITY;
+            if (kj + 32 > lim) s_cur[1][j] = -INFINITY;
+          }
+        }
+        // Online softmax in the exp2 domain on raw scores: with scale > 0,
+        // max(scale * s) = scale * max(s), and p = 2^(s * scale_log2 - ref). The reference point
+        // `ref` of o and l only moves when the row max has grown by more than kRescaleSlack over
+        // it, so probabilities stay at most 2^kRescaleSlack (no overflow; a bf16/fp16 P keeps its
+        // relative precision) and most tiles skip the rescale of o.
+        float mx = max_of(s_cur[0], s_cur[1]);
+        mx = fmaxf(mx, xor_lane(mx, 32));
+        const float cand = mx * sl2;  // -inf while the row has seen only hidden keys
+        move = cand > ref + kRescaleSlack;
+        alpha = move ? exp2_fast(ref - cand) : 1.f;  // ref = -inf gives 0
+        ref = move ? cand : ref;
+        // Rows without a visible key so far have only -inf scores: any finite shift gives p = 0.
+        const float shift = ref == -INFINITY ? 0.f : ref;
+        float rs0 = 0.f;
+        float rs1 = 0.f;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int kj = acc_key(j, half);
-        if (kj > lim) s0[j] = -INFINITY;
-        if (kj + 32 > lim) s1[j] = -INFINITY;
+        for (int j = 0; j < 16; ++j) {
+          s_cur[0][j] = exp2_fast(fmaf(s_cur[0][j], sl2, -shift));
+          s_cur[1][j] = exp2_fast(fmaf(s_cur[1][j], sl2, -shift));
+          rs0 += s_cur[0][j];
+          rs1 += s_cur[1][j];
+        }
+        l = fmaf(l, alpha, rs0 + rs1);
+        pf[0] = p_frag<Tag, 0>(s_cur[0]);
+        pf[1] = p_frag<Tag, 1>(s_cur[0]);
+        pf[2] = p_frag<Tag, 0>(s_cur[1]);
+        pf[3] = p_frag<Tag, 1>(s_cur[1]);
+#if FL_PREFILL_SCHED
+        // Interleave: K reads ahead, then one MFMA per group of VALU instructions.
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+#pragma unroll
+        for (int i = 0; i < D / 8 - 4; ++i) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedValu, FL_PREFILL_VALU_PER_MFMA, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedValu, FL_PREFILL_VALU_PER_MFMA, 0);
+        }
+#endif
+      };
+      const bool need_mask = (k0 + kBlockN > a.seqlen_k) ||
+                             (a.causal && k0 + kBlockN - 1 > row0 + a.causal_offset);
+      if (need_mask) {
+        step(std::true_type{});
+      } else {
+        step(std::false_type{});
       }
-    }
-
-    // Online softmax in the exp2 domain on raw scores: with scale > 0,
-    // max(scale * s) = scale * max(s), and p = 2^(s * scale_log2 - ref).
-    float mx = max_of(s0, s1);
-    mx = fmaxf(mx, xor_lane(mx, 32));
-    // The reference point `ref` (log2 units) of o and l only moves when the row max has grown by
-    // more than kRescaleSlack over it, so probabilities stay at most 2^kRescaleSlack: no overflow,
-    // and a bf16/fp16 P keeps its relative precision. Most tiles then skip the rescale of o.
-    const float cand = mx * sl2;  // -inf while the row has seen only hidden keys
-    const bool move = cand > ref + kRescaleSlack;
-    if (wave_any(move)) {
-      const float alpha = move ? exp2_fast(ref - cand) : 1.f;  // ref = -inf gives 0
-      ref = move ? cand : ref;
-      l *= alpha;
+      if (wave_any(move)) {
 #pragma unroll
-      for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
-    }
-    // Rows without a visible key so far have only -inf scores: any finite shift gives p = 0.
-    const float shift = ref == -INFINITY ? 0.f : ref;
-    float rs0 = 0.f;
-    float rs1 = 0.f;
+        for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
+      }
+      const uint16_t* vt = v_slot(t & 1);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      s0[j] = exp2_fast(fmaf(s0[j], sl2, -shift));
-      s1[j] = exp2_fast(fmaf(s1[j], sl2, -shift));
-      rs0 += s0[j];
-      rs1 += s1[j];
+      for (int nb = 0; nb < D / 32; ++nb) {
+        o[nb] = E::mfma32(v_frag<D>(vt, nb, 0, lane), pf[0], o[nb]);
+        o[nb] = E::mfma32(v_frag<D>(vt, nb, 1, lane), pf[1], o[nb]);
+        o[nb] = E::mfma32(v_frag<D>(vt, nb, 2, lane), pf[2], o[nb]);
+        o[nb] = E::mfma32(v_frag<D>(vt, nb, 3, lane), pf[3], o[nb]);
+      }
+#if FL_PREFILL_PIPELINE
+      s_cur[0] = s_next[0];
+      s_cur[1] = s_next[1];
+#endif
     }
-    l += rs0 + rs1;
-
-    const u32x4 p0 = p_frag<Tag, 0>(s0);
-    const u32x4 p1 = p_frag<Tag, 1>(s0);
-    const u32x4 p2 = p_frag<Tag, 0>(s1);
-    const u32x4 p3 = p_frag<Tag, 1>(s1);
-#pragma unroll
-    for (int nb = 0; nb < D / 32; ++nb) {
-      o[nb] = E::mfma32(v_frag<D>(vt, nb, 0, lane), p0, o[nb]);
-      o[nb] = E::mfma32(v_frag<D>(vt, nb, 1, lane), p1, o[nb]);
-      o[nb] = E::mfma32(v_frag<D>(vt, nb, 2, lane), p2, o[nb]);
-      o[nb] = E::mfma32(v_frag<D>(vt, nb, 3, lane), p3, o[nb]);
-    }
+    // The loads issued above have landed (the barrier waits for them) and every wave is done
+    // with the slots they overwrite next.
+    __syncthreads();
   }
 
   // Epilogue: l over both halves, 1/l (0 for rows that saw no key, which then store zeros).
@@ -263,7 +360,7 @@ __global__ void __launch_bounds__(64) mfma_tile_test_kernel(const uint16_t* a, c
   __syncthreads();
   if (!trans_b) {
     // b [16, k] is K (16 keys), a [16, k] is Q (16 query rows): S^T[key][row] = (a b^T)[row][key].
-    for (int i = lane; i < 16 * k; i += 64) tile[(i / k) * kPitch<D> + i % k] = b[i];
+    for (int i = lane; i < 16 * k; i += 64) tile[tile_offset<D>(i / k, i % k)] = b[i];
     __syncthreads();
     f32x16 s = f32x16{};
     for (int ks = 0; ks < k / 16; ++ks) {
@@ -284,7 +381,7 @@ __global__ void __launch_bounds__(64) mfma_tile_test_kernel(const uint16_t* a, c
     }
   } else {
     // b [k, 16] is V (k keys x 16 dims), a [16, k] is P: O^T[d][row] = (a b)[row][d].
-    for (int i = lane; i < k * 16; i += 64) tile[(i / 16) * kPitch<D> + i % 16] = b[i];
+    for (int i = lane; i < k * 16; i += 64) tile[tile_offset<D>(i / 16, i % 16)] = b[i];
     __syncthreads();
     f32x16 s0 = f32x16{};
     f32x16 s1 = f32x16{};

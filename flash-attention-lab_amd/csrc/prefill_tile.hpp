@@ -26,31 +26,50 @@ constexpr int kRowsPerWave = 32;
 constexpr int kBlockM = kRowsPerWave * kWaves;  // query rows per workgroup
 constexpr int kBlockN = 64;                     // keys per tile
 
-// LDS row pitch in elements: rows are padded by 16 bytes.
+// LDS tiles hold 64 rows of D elements with no padding. Within a row, 16-byte chunk c is stored
+// at chunk c ^ swz(r), an XOR swizzle chosen so that both LDS read patterns of the kernel are free
+// of bank conflicts on gfx950's 64 banks x 4 bytes (256 bytes per cycle):
+//  * K operand (ds_read_b128): 16 lanes read 16 consecutive rows at one logical chunk; swz is a
+//    bijection on each run of 16 rows, so they hit 16 distinct chunk positions.
+//  * V operand (ds_read_b64_tr_b16): 32 lanes read 4 consecutive rows x 4 chunks (an aligned
+//    group 4g..4g+3); swz moves each of the 4 rows to a different aligned group.
+// At D = 64 two rows share a 256-byte bank window, so the row parity takes part.
 template <int D>
-constexpr int kPitch = D + 8;
+constexpr int kPitch = D;
 template <int D>
 constexpr int kTileElems = kBlockN * kPitch<D>;
+
+template <int D>
+__device__ __forceinline__ constexpr int swz(int r) {
+  return D == 128 ? 4 * (r & 3) + ((r >> 2) & 3) : 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
+}
+
+// Element offset of (row, col) in a swizzled tile.
+template <int D>
+__device__ __forceinline__ constexpr int tile_offset(int r, int col) {
+  return r * kPitch<D> + 8 * ((col >> 3) ^ swz<D>(r)) + (col & 7);
+}
 
 // A operand of S^T += K Q^T for key block mb (32 keys) and dim step ks (16 dims):
 // lane l reads K[32 mb + l % 32][16 ks + 8 (l / 32) .. + 7], one 16-byte LDS read.
 template <int D>
 __device__ __forceinline__ u32x4 k_frag(const uint16_t* k_tile, int mb, int ks, int lane) {
-  const uint16_t* p = k_tile + (32 * mb + (lane & 31)) * kPitch<D> + 16 * ks + 8 * (lane >> 5);
+  const uint16_t* p = k_tile + tile_offset<D>(32 * mb + (lane & 31), 16 * ks + 8 * (lane >> 5));
   return *reinterpret_cast<const u32x4*>(p);
 }
 
 // A operand of O^T += V^T P^T for dim block nb (32 dims) and key step kk (16 keys): lane l needs
 // V[16 kk + 4 half + e][32 nb + l % 32] for e = 0..3, then the same 8 keys further on. Within
-// each 16-lane group, lane i addresses row i / 4 and columns 4 (i % 4) .. + 3 of the 4 x 16 block,
-// so that the transpose read hands lane i column i of all 4 rows.
+// each 16-lane group, lane i addresses row i / 4 and columns 4 (i % 4) .. + 3 of the 4 x 16 block
+// (8 contiguous bytes, which the swizzle keeps together), so that the transpose read hands lane i
+// column i of all 4 rows.
 template <int D>
 __device__ __forceinline__ u32x4 v_frag(const uint16_t* v_tile, int nb, int kk, int lane) {
   const int i = lane & 15;
-  const uint16_t* p = v_tile + (16 * kk + 4 * (lane >> 5) + (i >> 2)) * kPitch<D> + 32 * nb +
-                      16 * ((lane >> 4) & 1) + 4 * (i & 3);
-  const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr16(p));
-  const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr16(p + 8 * kPitch<D>));
+  const int r = 16 * kk + 4 * (lane >> 5) + (i >> 2);
+  const int col = 32 * nb + 16 * ((lane >> 4) & 1) + 4 * (i & 3);
+  const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr16(v_tile + tile_offset<D>(r, col)));
+  const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr16(v_tile + tile_offset<D>(r + 8, col)));
   return u32x4{lo.x, lo.y, hi.x, hi.y};
 }
 
