@@ -57,16 +57,6 @@ __device__ __forceinline__ int xcd_remap(int id, int n) {
 #ifndef FL_PREFILL_WAVES_PER_EU
 #define FL_PREFILL_WAVES_PER_EU 2
 #endif
-// Scheduling hints that interleave the next tile's score MFMAs with the softmax VALU work, and
-// the VALU instructions placed after each MFMA.
-#ifndef FL_PREFILL_SCHED
-#define FL_PREFILL_SCHED 0
-#endif
-// Software pipelining: the scores of tile t + 1 computed next to the softmax of tile t (costs a
-// second score buffer of 32 registers).
-#ifndef FL_PREFILL_PIPELINE
-#define FL_PREFILL_PIPELINE 0
-#endif
 // Scheduling groups that keep the K fragment reads ahead of the score MFMAs.
 #ifndef FL_PREFILL_QK_SCHED
 #define FL_PREFILL_QK_SCHED 1
@@ -75,11 +65,7 @@ __device__ __forceinline__ int xcd_remap(int id, int n) {
 #ifndef FL_PREFILL_K_AHEAD
 #define FL_PREFILL_K_AHEAD 2
 #endif
-#ifndef FL_PREFILL_VALU_PER_MFMA
-#define FL_PREFILL_VALU_PER_MFMA 8
-#endif
 // Instruction classes of __builtin_amdgcn_sched_group_barrier.
-constexpr int kSchedValu = 0x002;
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
 
@@ -89,10 +75,15 @@ __global__ void __launch_bounds__(kThreads)
     prefill_fwd_kernel(const PrefillArgs a) {
   using E = Elem<Tag>;
   constexpr int kTile = kTileElems<D>;
-  // Four tile slots: K tiles in slots 0 and 1, V tiles in slots 2 and 3.
-  __shared__ __attribute__((aligned(16))) uint16_t smem[4 * kTile];
-  auto k_slot = [&](int i) { return smem + i * kTile; };
-  auto v_slot = [&](int i) { return smem + (2 + i) * kTile; };
+  constexpr int kTileBytes = 2 * kTile;
+  // Two K and two V tile slots, each its own array: slot addresses are compile-time constants in
+  // the unrolled loop below (every LDS read is one per-lane offset register plus an immediate),
+  // and the compiler can tell that loads into one slot do not alias reads of another, so it does
+  // not wait for the next tile's loads before reading this tile.
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds0[kTile];
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds1[kTile];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds0[kTile];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds1[kTile];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -127,6 +118,17 @@ __global__ void __launch_bounds__(kThreads)
     for (int ks = 0; ks < D / 16; ++ks) qf[ks] = ok ? load16(src + 16 * ks) : u32x4{0, 0, 0, 0};
   }
 
+  // Per-lane LDS byte offsets within a tile (the swizzle makes them lane-dependent).
+  int k_lds[D / 16];
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) k_lds[ks] = k_lane_offset<D>(ks, lane);
+  int v_lds[D / 32][2];
+#pragma unroll
+  for (int nb = 0; nb < D / 32; ++nb) {
+    v_lds[nb][0] = v_lane_offset<D>(nb, 0, lane);
+    v_lds[nb][1] = v_lane_offset<D>(nb, 1, lane);
+  }
+
   // Tiles go from HBM straight into LDS (buffer_load ... lds): each wave moves kDmaPerWave
   // 1 KiB blocks of a tile; lane l's 16 bytes land at block + 16 l, so lane l fetches the
   // logical chunk that the swizzle stores at that position. The buffer resource is rebased on
@@ -144,11 +146,12 @@ __global__ void __launch_bounds__(kThreads)
     k_off[j] = static_cast<int>((row * a.k_ss + 8 * chunk) * 2);
     v_off[j] = static_cast<int>((row * a.v_ss + 8 * chunk) * 2);
   }
-  auto dma = [&](uint16_t* slot, const uint16_t* base, int64_t seq_stride, const int(&off)[kDmaPerWave],
-                 int tile) {
+  auto dma = [&](uint16_t* slot, const uint16_t* base, int64_t seq_stride,
+                 const int (&off)[kDmaPerWave], int tile) {
     const int k0 = tile * kBlockN;
     const int rows = min(kBlockN, a.seqlen_k - k0);
-    const auto rsrc = buffer_rsrc(base + k0 * seq_stride, static_cast<int>(((rows - 1) * seq_stride + D) * 2));
+    const auto rsrc =
+        buffer_rsrc(base + k0 * seq_stride, static_cast<int>(((rows - 1) * seq_stride + D) * 2));
 #pragma unroll
     for (int j = 0; j < kDmaPerWave; ++j)
       buffer_load16_to_lds(rsrc, slot + (wave * kDmaPerWave + j) * 512, off[j]);
@@ -163,165 +166,120 @@ __global__ void __launch_bounds__(kThreads)
   // Last key my_row may see in the whole problem.
   const int last_key = a.causal ? min(a.seqlen_k - 1, my_row + a.causal_offset) : a.seqlen_k - 1;
 
-  // S^T of the tile in k_tile for this wave's 32 rows. K fragments are read kKAhead steps ahead
-  // of the MFMAs that consume them, so the LDS latency overlaps the MFMA chain.
-  auto scores = [&](const uint16_t* k_tile, f32x16 (&s)[2]) {
-    constexpr int kSteps = D / 16;
-    constexpr int kAhead = FL_PREFILL_K_AHEAD < kSteps ? FL_PREFILL_K_AHEAD : kSteps;
-    u32x4 a0[kSteps];
-    u32x4 a1[kSteps];
-#pragma unroll
-    for (int ks = 0; ks < kAhead; ++ks) {
-      a0[ks] = k_frag<D>(k_tile, 0, ks, lane);
-      a1[ks] = k_frag<D>(k_tile, 1, ks, lane);
+  // One tile: loads of the next tile into the other slots, then (for a wave that sees any of its
+  // keys) scores, softmax and P V from slot kSlot, and a barrier after which the next tile's data
+  // is in LDS and this tile's slots are free.
+  auto tile_step = [&](int t, auto slot_tag) {
+    constexpr int kSlot = decltype(slot_tag)::value;
+    const char* kt = reinterpret_cast<const char*>(kSlot == 0 ? k_lds0 : k_lds1);
+    const char* vt = reinterpret_cast<const char*>(kSlot == 0 ? v_lds0 : v_lds1);
+    if (t + 1 < num_tiles) {
+      dma(kSlot == 0 ? k_lds1 : k_lds0, kp, a.k_ss, k_off, t + 1);
+      dma(kSlot == 0 ? v_lds1 : v_lds0, vp, a.v_ss, v_off, t + 1);
     }
-    s[0] = f32x16{};
-    s[1] = f32x16{};
-#pragma unroll
-    for (int ks = 0; ks < kSteps; ++ks) {
-      if (ks + kAhead < kSteps) {
-        a0[ks + kAhead] = k_frag<D>(k_tile, 0, ks + kAhead, lane);
-        a1[ks + kAhead] = k_frag<D>(k_tile, 1, ks + kAhead, lane);
-      }
-      s[0] = E::mfma32(a0[ks], qf[ks], s[0]);
-      s[1] = E::mfma32(a1[ks], qf[ks], s[1]);
-    }
-#if FL_PREFILL_QK_SCHED
-    // Keep the reads kAhead steps ahead: the scheduler otherwise pulls each read down to its
-    // MFMA and the LDS latency is exposed on every step.
-    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kAhead, 1);
-#pragma unroll
-    for (int ks = 0; ks < kSteps - kAhead; ++ks) {
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 1);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
-    }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * kAhead, 1);
-#endif
-  };
-
-  // Prologue: K and V of tile 0 and K of tile 1 in flight (then, pipelined, the scores of tile 0).
-  f32x16 s_cur[2];
-  if (num_tiles > 0) {
-    dma(k_slot(0), kp, a.k_ss, k_off, 0);
-    dma(v_slot(0), vp, a.v_ss, v_off, 0);
-#if FL_PREFILL_PIPELINE
-    if (num_tiles > 1) dma(k_slot(1), kp, a.k_ss, k_off, 1);
-#endif
-    __syncthreads();
-#if FL_PREFILL_PIPELINE
-    scores(k_slot(0), s_cur);
-#endif
-  }
-
-  // Iteration t: scores, softmax and P V of tile t while the next tile's loads are in flight; each
-  // load goes to the slot of tile t - 1, which every wave finished with before the last barrier.
-  // Pipelined, the scores of tile t + 1 (MFMA) are computed in the same straight-line block as the
-  // softmax of tile t (VALU) so the two interleave; K then runs two tiles ahead: K(t + 2) goes to
-  // K(t)'s slot, whose scores were computed in the previous iteration.
-  for (int t = 0; t < num_tiles; ++t) {
-#if FL_PREFILL_PIPELINE
-    if (t + 2 < num_tiles) dma(k_slot(t & 1), kp, a.k_ss, k_off, t + 2);
-#else
-    if (t + 1 < num_tiles) dma(k_slot((t + 1) & 1), kp, a.k_ss, k_off, t + 1);
-#endif
-    if (t + 1 < num_tiles) dma(v_slot((t + 1) & 1), vp, a.v_ss, v_off, t + 1);
-
     const int k0 = t * kBlockN;
     // A wave that sees no key of this tile sees none of the later ones either (causal).
     const bool active = !(a.causal && k0 > row0 + kRowsPerWave - 1 + a.causal_offset);
     if (active) {
-#if FL_PREFILL_PIPELINE
-      f32x16 s_next[2];
-#endif
-      u32x4 pf[4];
-      bool move;
-      float alpha;
-      auto step = [&](auto masked) {
-#if FL_PREFILL_PIPELINE
-        // Scores of tile t + 1. On the last tile the slot holds stale data; the result is unused.
-        scores(k_slot((t + 1) & 1), s_next);
-#else
-        scores(k_slot(t & 1), s_cur);
-#endif
-        if constexpr (decltype(masked)::value) {
-          const int lim = last_key - k0;
+      // S^T = K Q^T, K fragments read kAhead steps ahead of their MFMAs.
+      constexpr int kSteps = D / 16;
+      constexpr int kAhead = FL_PREFILL_K_AHEAD < kSteps ? FL_PREFILL_K_AHEAD : kSteps;
+      f32x16 s0 = f32x16{};
+      f32x16 s1 = f32x16{};
+      {
+        u32x4 a0[kSteps];
+        u32x4 a1[kSteps];
 #pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int kj = acc_key(j, half);
-            if (kj > lim) s_cur[0][j] = -INFINITY;
-            if (kj + 32 > lim) s_cur[1][j] = -INFINITY;
-          }
+        for (int ks = 0; ks < kAhead; ++ks) {
+          a0[ks] = lds_load16(kt, k_lds[ks]);
+          a1[ks] = lds_load16(kt + kKeyBlockBytes<D>, k_lds[ks]);
         }
-        // Online softmax in the exp2 domain on raw scores: with scale > 0,
-        // max(scale * s) = scale * max(s), and p = 2^(s * scale_log2 - ref). The reference point
-        // `ref` of o and l only moves when the row max has grown by more than kRescaleSlack over
-        // it, so probabilities stay at most 2^kRescaleSlack (no overflow; a bf16/fp16 P keeps its
-        // relative precision) and most tiles skip the rescale of o.
-        float mx = max_of(s_cur[0], s_cur[1]);
-        mx = fmaxf(mx, xor_lane(mx, 32));
-        const float cand = mx * sl2;  // -inf while the row has seen only hidden keys
-        move = cand > ref + kRescaleSlack;
-        alpha = move ? exp2_fast(ref - cand) : 1.f;  // ref = -inf gives 0
-        ref = move ? cand : ref;
-        // Rows without a visible key so far have only -inf scores: any finite shift gives p = 0.
-        const float shift = ref == -INFINITY ? 0.f : ref;
-        float rs0 = 0.f;
-        float rs1 = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < kSteps; ++ks) {
+          if (ks + kAhead < kSteps) {
+            a0[ks + kAhead] = lds_load16(kt, k_lds[ks + kAhead]);
+            a1[ks + kAhead] = lds_load16(kt + kKeyBlockBytes<D>, k_lds[ks + kAhead]);
+          }
+          s0 = E::mfma32(a0[ks], qf[ks], s0);
+          s1 = E::mfma32(a1[ks], qf[ks], s1);
+        }
+#if FL_PREFILL_QK_SCHED
+        // Keep the reads kAhead steps ahead: the scheduler otherwise pulls each read down to its
+        // MFMA and the LDS latency is exposed on every step.
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kAhead, 1);
+#pragma unroll
+        for (int ks = 0; ks < kSteps - kAhead; ++ks) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 1);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * kAhead, 1);
+#endif
+      }
+      // Keys past the end or above the diagonal: only edge and diagonal tiles (wave-uniform
+      // branch; the empty asm keeps the compiler from turning it into selects on every tile).
+      if ((k0 + kBlockN > a.seqlen_k) ||
+          (a.causal && k0 + kBlockN - 1 > row0 + a.causal_offset)) {
+        asm volatile("" ::: "memory");
+        const int lim = last_key - k0;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          s_cur[0][j] = exp2_fast(fmaf(s_cur[0][j], sl2, -shift));
-          s_cur[1][j] = exp2_fast(fmaf(s_cur[1][j], sl2, -shift));
-          rs0 += s_cur[0][j];
-          rs1 += s_cur[1][j];
+          const int kj = acc_key(j, half);
+          if (kj > lim) s0[j] = -INFINITY;
+          if (kj + 32 > lim) s1[j] = -INFINITY;
         }
-        l = fmaf(l, alpha, rs0 + rs1);
-        pf[0] = p_frag<Tag, 0>(s_cur[0]);
-        pf[1] = p_frag<Tag, 1>(s_cur[0]);
-        pf[2] = p_frag<Tag, 0>(s_cur[1]);
-        pf[3] = p_frag<Tag, 1>(s_cur[1]);
-#if FL_PREFILL_SCHED
-        // Interleave: K reads ahead, then one MFMA per group of VALU instructions.
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
-#pragma unroll
-        for (int i = 0; i < D / 8 - 4; ++i) {
-          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(kSchedValu, FL_PREFILL_VALU_PER_MFMA, 0);
-          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(kSchedValu, FL_PREFILL_VALU_PER_MFMA, 0);
-        }
-#endif
-      };
-      const bool need_mask = (k0 + kBlockN > a.seqlen_k) ||
-                             (a.causal && k0 + kBlockN - 1 > row0 + a.causal_offset);
-      if (need_mask) {
-        step(std::true_type{});
-      } else {
-        step(std::false_type{});
       }
+      // Online softmax in the exp2 domain on raw scores: with scale > 0,
+      // max(scale * s) = scale * max(s), and p = 2^(s * scale_log2 - ref). The reference point
+      // `ref` of o and l only moves when the row max has grown by more than kRescaleSlack over
+      // it, so probabilities stay at most 2^kRescaleSlack (no overflow; a bf16/fp16 P keeps its
+      // relative precision) and most tiles skip the rescale of o.
+      float mx = max_of(s0, s1);
+      mx = fmaxf(mx, xor_lane(mx, 32));
+      const float cand = mx * sl2;  // -inf while the row has seen only hidden keys
+      const bool move = cand > ref + kRescaleSlack;
+      const float alpha = move ? exp2_fast(ref - cand) : 1.f;  // ref = -inf gives 0
+      ref = move ? cand : ref;
       if (wave_any(move)) {
+        asm volatile("" ::: "memory");
 #pragma unroll
         for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
       }
-      const uint16_t* vt = v_slot(t & 1);
+      // Rows without a visible key so far have only -inf scores: any finite shift gives p = 0.
+      const float shift = ref == -INFINITY ? 0.f : ref;
+      float rs0 = 0.f;
+      float rs1 = 0.f;
 #pragma unroll
-      for (int nb = 0; nb < D / 32; ++nb) {
-        o[nb] = E::mfma32(v_frag<D>(vt, nb, 0, lane), pf[0], o[nb]);
-        o[nb] = E::mfma32(v_frag<D>(vt, nb, 1, lane), pf[1], o[nb]);
-        o[nb] = E::mfma32(v_frag<D>(vt, nb, 2, lane), pf[2], o[nb]);
-        o[nb] = E::mfma32(v_frag<D>(vt, nb, 3, lane), pf[3], o[nb]);
+      for (int j = 0; j < 16; ++j) {
+        s0[j] = exp2_fast(fmaf(s0[j], sl2, -shift));
+        s1[j] = exp2_fast(fmaf(s1[j], sl2, -shift));
+        rs0 += s0[j];
+        rs1 += s1[j];
       }
-#if FL_PREFILL_PIPELINE
-      s_cur[0] = s_next[0];
-      s_cur[1] = s_next[1];
-#endif
+      l = fmaf(l, alpha, rs0 + rs1);
+      const u32x4 pf[4] = {p_frag<Tag, 0>(s0), p_frag<Tag, 1>(s0), p_frag<Tag, 0>(s1),
+                           p_frag<Tag, 1>(s1)};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+        for (int nb = 0; nb < D / 32; ++nb) {
+          const u32x4 vf = v_frag_at(vt + kk * kKeyStepBytes<D>, v_lds[nb][0], v_lds[nb][1]);
+          o[nb] = E::mfma32(vf, pf[kk], o[nb]);
+        }
+      }
     }
     // The loads issued above have landed (the barrier waits for them) and every wave is done
-    // with the slots they overwrite next.
+    // with this tile's slots.
     __syncthreads();
+  };
+
+  if (num_tiles > 0) {
+    dma(k_lds0, kp, a.k_ss, k_off, 0);
+    dma(v_lds0, vp, a.v_ss, v_off, 0);
+    __syncthreads();
+  }
+  for (int t = 0; t < num_tiles; t += 2) {
+    tile_step(t, std::integral_constant<int, 0>{});
+    if (t + 1 < num_tiles) tile_step(t + 1, std::integral_constant<int, 1>{});
   }
 
   // Epilogue: l over both halves, 1/l (0 for rows that saw no key, which then store zeros).

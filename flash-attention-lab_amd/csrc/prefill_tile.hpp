@@ -50,27 +50,52 @@ __device__ __forceinline__ constexpr int tile_offset(int r, int col) {
   return r * kPitch<D> + 8 * ((col >> 3) ^ swz<D>(r)) + (col & 7);
 }
 
+// Byte offset in a tile of lane l's K operand piece for dim step ks: row l % 32, dims
+// 16 ks + 8 (l / 32) .. + 7 (key block mb adds 32 rows, a fixed offset since swz(r + 32) = swz(r)).
+template <int D>
+__device__ __forceinline__ int k_lane_offset(int ks, int lane) {
+  return 2 * tile_offset<D>(lane & 31, 16 * ks + 8 * (lane >> 5));
+}
+template <int D>
+constexpr int kKeyBlockBytes = 32 * kPitch<D> * 2;
+
+// Byte offset of lane l's first transpose read of the V operand for dim block nb (the second read,
+// 8 rows further, is `hi`). Within each 16-lane group, lane i addresses row i / 4 and columns
+// 4 (i % 4) .. + 3 of a 4 x 16 block (8 contiguous bytes, which the swizzle keeps together), so
+// that the transpose read hands lane i column i of all 4 rows. Key step kk adds 16 rows, a fixed
+// offset since swz(r + 16) = swz(r).
+template <int D>
+__device__ __forceinline__ int v_lane_offset(int nb, int hi, int lane) {
+  const int i = lane & 15;
+  const int r = 4 * (lane >> 5) + (i >> 2) + 8 * hi;
+  const int col = 32 * nb + 16 * ((lane >> 4) & 1) + 4 * (i & 3);
+  return 2 * tile_offset<D>(r, col);
+}
+template <int D>
+constexpr int kKeyStepBytes = 16 * kPitch<D> * 2;
+
+__device__ __forceinline__ u32x4 lds_load16(const void* base, int byte_offset) {
+  return *reinterpret_cast<const u32x4*>(static_cast<const char*>(base) + byte_offset);
+}
+
 // A operand of S^T += K Q^T for key block mb (32 keys) and dim step ks (16 dims):
 // lane l reads K[32 mb + l % 32][16 ks + 8 (l / 32) .. + 7], one 16-byte LDS read.
 template <int D>
 __device__ __forceinline__ u32x4 k_frag(const uint16_t* k_tile, int mb, int ks, int lane) {
-  const uint16_t* p = k_tile + tile_offset<D>(32 * mb + (lane & 31), 16 * ks + 8 * (lane >> 5));
-  return *reinterpret_cast<const u32x4*>(p);
+  return lds_load16(k_tile, mb * kKeyBlockBytes<D> + k_lane_offset<D>(ks, lane));
 }
 
 // A operand of O^T += V^T P^T for dim block nb (32 dims) and key step kk (16 keys): lane l needs
-// V[16 kk + 4 half + e][32 nb + l % 32] for e = 0..3, then the same 8 keys further on. Within
-// each 16-lane group, lane i addresses row i / 4 and columns 4 (i % 4) .. + 3 of the 4 x 16 block
-// (8 contiguous bytes, which the swizzle keeps together), so that the transpose read hands lane i
-// column i of all 4 rows.
+// V[16 kk + 4 half + e][32 nb + l % 32] for e = 0..3, then the same for the 4 keys 8 rows on.
+__device__ __forceinline__ u32x4 v_frag_at(const void* v_tile, int lo_offset, int hi_offset) {
+  const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr16(static_cast<const char*>(v_tile) + lo_offset));
+  const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr16(static_cast<const char*>(v_tile) + hi_offset));
+  return u32x4{lo.x, lo.y, hi.x, hi.y};
+}
 template <int D>
 __device__ __forceinline__ u32x4 v_frag(const uint16_t* v_tile, int nb, int kk, int lane) {
-  const int i = lane & 15;
-  const int r = 16 * kk + 4 * (lane >> 5) + (i >> 2);
-  const int col = 32 * nb + 16 * ((lane >> 4) & 1) + 4 * (i & 3);
-  const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr16(v_tile + tile_offset<D>(r, col)));
-  const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr16(v_tile + tile_offset<D>(r + 8, col)));
-  return u32x4{lo.x, lo.y, hi.x, hi.y};
+  return v_frag_at(v_tile, kk * kKeyStepBytes<D> + v_lane_offset<D>(nb, 0, lane),
+                   kk * kKeyStepBytes<D> + v_lane_offset<D>(nb, 1, lane));
 }
 
 // B operand of O^T += V^T P^T for key step kk from the probabilities of key block kk / 2:
