@@ -111,6 +111,29 @@ __device__ __forceinline__ void buffer_load16_to_lds(__amdgpu_buffer_rsrc_t rsrc
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(lds_block), 16, offset, 0, 0, 0);
 }
 
+// The same load issued from inline assembly: the compiler does not see it, so it inserts no
+// waits of its own for later LDS reads. The caller orders it with explicit s_waitcnt vmcnt and
+// barriers. `words` is a raw buffer resource (base, num_records, kBufferRsrcWord3), `lds_addr` the
+// wave-uniform LDS byte address of the 1 KiB block (lane l writes 16 bytes at lds_addr + 16 l).
+typedef uint32_t u32x4s __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4s buffer_words(const void* base, uint32_t bytes) {
+  const uint64_t addr = reinterpret_cast<uint64_t>(base);
+  return u32x4s{static_cast<uint32_t>(addr), static_cast<uint32_t>(addr >> 32) & 0xffffu, bytes,
+                static_cast<uint32_t>(kBufferRsrcWord3)};
+}
+__device__ __forceinline__ void buffer_load16_to_lds_asm(u32x4s words, uint32_t lds_addr,
+                                                         int offset) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
+               :
+               : "v"(offset), "s"(lds_addr), "s"(words)
+               : "memory", "m0");
+}
+// 32-bit LDS address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  typedef __attribute__((address_space(3))) const void lds_cvoid;
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_cvoid*)(p)));
+}
+
 // True on every lane when `pred` holds on any active lane (a wave-uniform branch condition).
 __device__ __forceinline__ bool wave_any(bool pred) {
   return __builtin_amdgcn_ballot_w64(pred) != 0;

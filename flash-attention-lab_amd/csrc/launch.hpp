@@ -56,6 +56,9 @@ constexpr int kPrefillBlockM = 128;
 constexpr int kPrefillBlockN = 64;
 
 hipError_t launch_prefill(const PrefillArgs& args, DType dtype, int head_dim, hipStream_t stream);
+// Ping-pong variant (head_dim 128 only): 8 waves, 256 query rows per workgroup.
+hipError_t launch_prefill_pingpong(const PrefillArgs& args, DType dtype, int head_dim,
+                                   hipStream_t stream);
 
 // Query heads one decode workgroup serves for a GQA group size (a power of two dividing it).
 int decode_heads_per_workgroup(int group);

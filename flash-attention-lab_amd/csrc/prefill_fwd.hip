@@ -220,10 +220,13 @@ __global__ void __launch_bounds__(kThreads)
       if ((k0 + kBlockN > a.seqlen_k) ||
           (a.causal && k0 + kBlockN - 1 > row0 + a.causal_offset)) {
         asm volatile("" ::: "memory");
-        const int lim = last_key - k0;
+        // acc_key(j, half) = acc_key(j, 0) + 4 half: fold the lane's part into the limit so every
+        // comparison is against a compile-time constant (no per-key registers live in the loop).
+        const int lim = last_key - k0 - 4 * half;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          const int kj = acc_key(j, half);
+          constexpr int kBase = 0;
+          const int kj = acc_key(j, kBase);
           if (kj > lim) s0[j] = -INFINITY;
           if (kj + 32 > lim) s1[j] = -INFINITY;
         }
@@ -374,8 +377,15 @@ hipError_t launch_typed(const PrefillArgs& args, hipStream_t stream) {
 static_assert(kPrefillBlockM == prefill::kBlockM, "host and kernel tile heights differ");
 static_assert(kPrefillBlockN == prefill::kBlockN, "host and kernel tile widths differ");
 
+// head_dim 128 runs on the ping-pong kernel (prefill_pp.hip); FL_PREFILL_PINGPONG=0 keeps it on this
+// one (for comparisons).
+#ifndef FL_PREFILL_PINGPONG
+#define FL_PREFILL_PINGPONG 1
+#endif
+
 hipError_t launch_prefill(const PrefillArgs& args, DType dtype, int head_dim, hipStream_t stream) {
   using namespace prefill;
+  if (FL_PREFILL_PINGPONG && head_dim == 128) return launch_prefill_pingpong(args, dtype, head_dim, stream);
   if (dtype == DType::bf16) {
     return head_dim == 64 ? launch_typed<bf16_tag, 64>(args, stream)
                           : launch_typed<bf16_tag, 128>(args, stream);
