@@ -93,7 +93,7 @@ def cpu_model() -> str:
     return "unknown"
 
 
-TRAFFIC_PROFILE = REPO / "profiles" / "prefill_fwd_4x32x32x4096x128_bf16.md"
+TRAFFIC_PROFILE = REPO / "profiles" / "prefill_pp_kernel_4x32x32x4096x128_bf16.md"
 
 
 def profiled_traffic(path: Path = TRAFFIC_PROFILE) -> float | None:
@@ -260,6 +260,10 @@ def bench_decode(name: str, steps: int, warmup: int, flush) -> dict:
         "gbps": kv / (stats["median"] / 1e3) / 1e9,
         "gbps_mean": kv / (mean_ms / 1e3) / 1e9,
         "frac_of_peak": kv / (mean_ms / 1e3) / 1e9 / PEAK_HBM_GBPS,
+        "roofline": {"bound": "hbm", "achieved": kv / (mean_ms / 1e3) / 1e9, "peak": PEAK_HBM_GBPS,
+                     "unit": "GB/s", "frac": kv / (mean_ms / 1e3) / 1e9 / PEAK_HBM_GBPS,
+                     "per_launch": f"{kv:.4g} B of K+V (every cached row once), mean {mean_ms:.4f} ms "
+                                   "for the split and merge kernels"},
         "max_err_vs_fp64": err,
         "max_err_torch_vs_fp64": err_torch,
     }
@@ -409,7 +413,7 @@ def main(argv=None) -> int:
             "frac": headline["tflops_mean"] / PEAK_BF16_TFLOPS,
             "traffic": profiled_traffic(),
             "traffic_source": str(TRAFFIC_PROFILE.relative_to(REPO)),
-            "kernel": "prefill_fwd_kernel<bf16_tag, 128>",
+            "kernel": "prefill_pp_kernel<bf16_tag, 128>",
             "per_launch": f"{headline['flops']:.4g} FLOP (4 B H S^2 D), mean {headline['mean_ms']:.4f} ms",
         }
     else:

@@ -10,22 +10,25 @@
 // Why: within one wave, VALU instructions issued between MFMAs do not overlap with them (on gfx950
 // an MFMA followed by 8 independent FMAs takes as long as the two back to back), while an MFMA
 // stream in one wave and a VALU stream in another wave of the same SIMD run concurrently at full
-// MFMA rate. The softmax (about 150 VALU instructions per 32 x 64 tile, 32 of them exp) therefore
-// only hides behind MFMAs if another wave on the same SIMD is in its MFMA phase at that moment.
+// MFMA rate. A wave issues at most one instruction every 4-5 cycles whatever its kind, so the
+// softmax wave's phase costs about 5 cycles per instruction (about 9.6 per exponential) and must
+// stay below the MFMA phase's 1024 cycles: everything that is not softmax arithmetic (tile loads,
+// their descriptors) is issued by the MFMA wave, which has idle issue slots while its MFMAs run.
 //
 //  * Workgroup: 8 waves x 32 query rows = 256 rows of one (batch, head). Waves w and w + 4 share a
 //    SIMD (the dispatcher deals waves to SIMDs with period 4). Group 0 is waves 0-3, group 1 waves
 //    4-7: one wave of each group per SIMD.
 //  * Time is cut into half-periods by workgroup barriers. In half-period 2m group 0 runs
 //    MFMA(m) = P V of tile m-1 then S = K Q^T of tile m (32 MFMAs) while group 1 runs the softmax
-//    of tile m-1; in half-period 2m+1 the roles swap. Each MFMA phase is 32 MFMAs (1024 MFMA
-//    cycles at D = 128), each softmax phase about 800 cycles of VALU issue, so the MFMA pipe of
-//    every SIMD is fed by one wave or the other all the time.
+//    of tile m-1; in half-period 2m+1 the roles swap.
 //  * K and V tiles (64 keys) stream through a ring of kStages LDS slots each, filled by direct
-//    global -> LDS loads (buffer_load ... lds) that group 1 issues at the start of its softmax
-//    phases, 2 kStages - 3 half-periods before the data is needed. Load batch b = {K(b), V(b-1)}.
-//    Loads past the last tile use an empty buffer resource (they write zeros into a free slot)
-//    so every wave issues the same number of loads and the vmcnt accounting is uniform.
+//    global -> LDS loads (buffer_load ... lds) issued between the MFMAs of the MFMA phases: group 0
+//    loads K(m + kStages - 1) in half-period 2m, group 1 V(m + kStages - 2) in half-period 2m+1
+//    (4 loads per wave each; a load costs the issuing wave about 70 cycles, which the MFMA phase
+//    has to spare). Each group waits for its own tiles at the end of its softmax phase just before
+//    they are first read. Loads past the last tile use an empty buffer resource (they write zeros
+//    into a free slot) so every wave issues the same number of loads and the vmcnt accounting is
+//    uniform.
 //  * Work order as in prefill_fwd.hip: XCD-contiguous (batch, head) ranges; causal query blocks
 //    heaviest first.
 #include <type_traits>
@@ -41,19 +44,24 @@ namespace {
 constexpr int kPpWaves = 8;
 constexpr int kPpThreads = 64 * kPpWaves;
 constexpr int kPpBlockM = kRowsPerWave * kPpWaves;  // 256 query rows per workgroup
-constexpr int kLoadWaves = 4;                       // group 1 issues the tile loads
+constexpr int kLoadWaves = 4;                       // waves per group: one group per tensor
 constexpr int kXcds = 8;
 constexpr float kLn2 = 0.693147180559945309f;
-constexpr float kRescaleSlack = 8.f;
+// Largest lane sum of probabilities (32 of them) kept without moving the reference point.
+constexpr float kSumLimit = 32768.f;
+// Reference point of a row that has not seen a score yet: finite, so p = 2^(s scale_log2 - ref)
+// overflows (sum above kSumLimit: the first tile with a key takes the max path) and masked scores
+// still give 0, with no separate test for "no reference yet".
+constexpr float kNoRef = -1e30f;
 
-// LDS ring depth (K and V slots each). A load batch is issued 2 kStages - 2 half-periods before
-// the half-period that first reads it, and must land 2 kStages - 3 half-periods after issue.
+// LDS ring depth (K and V slots each). A tile is issued 2 kStages - 4 (K) or 2 kStages - 5 (V)
+// half-periods before the half-period that first reads it.
 #ifndef FL_PP_STAGES
-#define FL_PP_STAGES 3
+#define FL_PP_STAGES 4
 #endif
 constexpr int kStages = FL_PP_STAGES;
-static_assert(kStages == 2 || kStages == 3 || kStages == 4, "2 to 4 ring stages");
-// Raise the issue priority of the wave in its MFMA phase.
+static_assert(kStages == 3 || kStages == 4, "3 or 4 ring stages");
+// Raise the issue priority of the wave in its MFMA phase (1) or in its softmax phase (2).
 #ifndef FL_PP_SETPRIO
 #define FL_PP_SETPRIO 1
 #endif
@@ -111,12 +119,11 @@ __device__ __forceinline__ void phase_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// Waits until at most kCount of this wave's vector-memory loads are in flight.
 template <int kCount>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(kCount >= 0 && kCount <= 63, "vmcnt range");
-  if constexpr (kCount == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if constexpr (kCount == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  if constexpr (kCount == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kCount) : "memory");
 }
 
 template <typename Tag, int D>
@@ -130,11 +137,8 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * kStages * kTile];
   constexpr int kSlotBytes = 2 * kTile;
   constexpr int kVRingBytes = kStages * kSlotBytes;
-  static_assert((kStages - 1) * kSlotBytes + kSlotBytes <= 65536, "K ring must fit the immediate range");
+  static_assert(kVRingBytes <= 65536, "K ring must fit the immediate range");
   auto k_slot = [&](auto s) -> uint16_t* { return smem + (decltype(s)::value % kStages) * kTile; };
-  auto v_slot = [&](auto s) -> uint16_t* {
-    return smem + (kStages + decltype(s)::value % kStages) * kTile;
-  };
   // Byte offset of V slot s from the biased per-lane V offsets.
   auto v_slot_offset = [&](auto s) constexpr { return (decltype(s)::value % kStages) * kSlotBytes; };
   const char* lds_bytes = reinterpret_cast<const char*>(smem);
@@ -163,11 +167,16 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   int kv_end = a.seqlen_k;
   if (a.causal) kv_end = min(kv_end, min(q0 + kPpBlockM, a.seqlen_q) + a.causal_offset);
   const int num_tiles = kv_end > 0 ? (kv_end + kBlockN - 1) / kBlockN : 0;
-  // Tiles this wave sees any key of (a prefix of the workgroup's tiles).
+  // Tiles this wave sees any key of (a prefix of the workgroup's tiles), and the first tile whose
+  // scores need masking (it reaches past the sequence end or, causal, past the diagonal of the
+  // wave's first row): every tile before it is fully visible to every row of the wave.
   int my_tiles = num_tiles;
+  int mask_from = a.seqlen_k / kBlockN;
   if (a.causal) {
     const int last = row0 + kRowsPerWave - 1 + a.causal_offset;  // last key any of its rows sees
     my_tiles = last < 0 ? 0 : min(num_tiles, last / kBlockN + 1);
+    const int x = row0 + a.causal_offset - (kBlockN - 1);  // tile t needs masking iff 64 t > x
+    mask_from = min(mask_from, x < 0 ? 0 : x / kBlockN + 1);
   }
 
   u32x4 qf[D / 16];
@@ -194,40 +203,47 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     v_lds[nb][1] = v_lane_offset<D>(nb, 1, lane) + v_bias;
   }
 
-  // Tile loads (group 1 only): each load wave moves kDmaPerWave 1 KiB blocks of a tile.
+  // Tile loads: group 0 streams the K tiles, group 1 the V tiles. Wave lw of a group moves
+  // kDmaPerWave 1 KiB blocks of each tile; block j of a slot sits at LDS byte lds_wave + slot
+  // offset + 1024 j, and its lane l covers row (lw kDmaPerWave + j) kRowsPerBlock + l /
+  // kChunksPerRow, chunk l % kChunksPerRow (stored swizzled).
   constexpr int kChunksPerRow = D / 8;
   constexpr int kRowsPerBlock = 64 / kChunksPerRow;
   constexpr int kDmaPerWave = kBlockN / kRowsPerBlock / kLoadWaves;
   const int lw = wave & 3;
-  int k_off[kDmaPerWave];
-  int v_off[kDmaPerWave];
+  const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(
+      lds_address(smem) + (group == 0 ? 0 : kVRingBytes) + lw * kDmaPerWave * 1024);
+  const uint16_t* my_base = group == 0 ? kp : vp;
+  const int64_t my_ss = group == 0 ? a.k_ss : a.v_ss;
+  int my_off[kDmaPerWave];
 #pragma unroll
   for (int j = 0; j < kDmaPerWave; ++j) {
     const int row = (lw * kDmaPerWave + j) * kRowsPerBlock + lane / kChunksPerRow;
     const int chunk = (lane % kChunksPerRow) ^ swz<D>(row);
-    k_off[j] = static_cast<int>((row * a.k_ss + 8 * chunk) * 2);
-    v_off[j] = static_cast<int>((row * a.v_ss + 8 * chunk) * 2);
+    my_off[j] = static_cast<int>((row * my_ss + 8 * chunk) * 2);
   }
-  // Loads of one tensor's tile `tile` into `slot`; tiles outside [0, num_tiles) use an empty
-  // resource and write zeros.
-  // Loads of one tensor's tile `tile` into `slot` (inline assembly: ordered only by the explicit
-  // waits and barriers of the schedule below); tiles outside [0, num_tiles) use an empty resource
-  // and write zeros.
-  auto dma = [&](uint16_t* slot, const uint16_t* base, int64_t seq_stride, const int (&off)[kDmaPerWave],
-                 int tile) {
-    const int k0 = tile * kBlockN;
-    const int rows = (tile >= 0 && tile < num_tiles) ? min(kBlockN, a.seqlen_k - k0) : 0;
-    const uint16_t* tile_base = rows > 0 ? base + k0 * seq_stride : base;
-    const uint32_t bytes = rows > 0 ? static_cast<uint32_t>(((rows - 1) * seq_stride + D) * 2) : 0u;
-    const u32x4s words = buffer_words(tile_base, bytes);
-    const uint32_t lds0 = lds_address(slot) + lw * kDmaPerWave * 1024;
-#pragma unroll
-    for (int j = 0; j < kDmaPerWave; ++j) buffer_load16_to_lds_asm(words, lds0 + j * 1024, off[j]);
+  // Buffer resource of tile t of the group's tensor: based at the tile's first row, sized to its
+  // valid rows (full tiles before the last one, the last one up to the sequence end, none outside
+  // [0, num_tiles): those read as zeros).
+  const int64_t tile_bytes = static_cast<int64_t>(kBlockN) * my_ss * 2;
+  const int last_rows = num_tiles > 0 ? min(kBlockN, a.seqlen_k - (num_tiles - 1) * kBlockN) : 1;
+  const uint32_t full_bytes = static_cast<uint32_t>(((kBlockN - 1) * my_ss + D) * 2);
+  const uint32_t last_bytes = static_cast<uint32_t>(((last_rows - 1) * my_ss + D) * 2);
+  auto tile_words = [&](int t) -> u32x4s {
+    const bool inside = t >= 0 && t < num_tiles;
+    const uint32_t bytes = !inside ? 0u : t == num_tiles - 1 ? last_bytes : full_bytes;
+    const char* p = reinterpret_cast<const char*>(my_base) + (inside ? t * tile_bytes : 0);
+    return buffer_words(p, bytes);
   };
-  // Load batch bt = {K(bt), V(bt - 1)} into their ring slots.
-  auto load_batch = [&](int bt, auto kslot_tag, auto vslot_tag) {
-    dma(k_slot(kslot_tag), kp, a.k_ss, k_off, bt);
-    dma(v_slot(vslot_tag), vp, a.v_ss, v_off, bt - 1);
+  // Block j of the group's tile (descriptor `w`) into ring slot kSlot.
+  auto issue_block = [&](u32x4s w, auto slot_tag, auto j_tag) {
+    constexpr int j = decltype(j_tag)::value;
+    constexpr uint32_t kOff = (decltype(slot_tag)::value % kStages) * kSlotBytes + j * 1024;
+    buffer_load16_to_lds_asm(w, lds_wave + kOff, my_off[j]);
+  };
+  auto load_tile = [&](int t, auto slot_tag) {
+    const u32x4s w = tile_words(t);
+    static_for<0, kDmaPerWave>([&](auto j) { issue_block(w, slot_tag, j); });
   };
 
   f32x16 o[D / 32];
@@ -236,37 +252,44 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   f32x16 s0 = f32x16{};
   f32x16 s1 = f32x16{};
   u32x4 pf[4] = {};
-  float ref = -INFINITY;
+  float ref = kNoRef;
   float l = 0.f;
   const float sl2 = a.scale_log2;
   const int last_key = a.causal ? min(a.seqlen_k - 1, my_row + a.causal_offset) : a.seqlen_k - 1;
 
-  // MFMA phase of period m: O += V(m-1) P(m-1), then S = K(m) Q^T.
   // MFMA phase of a period with slots kS = m % kStages: O += V(m-1) P(m-1) (16 MFMAs), then
   // S = K(m) Q^T (16 MFMAs). No branches: in period 0 the previous P and V are zeros (P starts at
   // 0, the V slot was filled from an empty resource), a skipped softmax leaves P = 0, and scores of
   // tiles nobody reads are never used. The 32 MFMAs form one software pipeline: the A-operand
   // fragment of MFMA i + kAhead is read from LDS right after MFMA i issues, and a scheduling
   // barrier after every step keeps that order (left to itself the scheduler reads each fragment
-  // just before its MFMA and the LDS latency shows on every step).
-  auto mfma_phase = [&](auto slot_tag) {
+  // just before its MFMA and the LDS latency shows on every step). The first kAhead fragments are
+  // read at the end of the wave's softmax phase (prefetch), so the MFMA phase starts without
+  // waiting for LDS. hook(i) runs after MFMA i (the tile loads are issued there).
+  constexpr int kPv = 4 * (D / 32);  // P V MFMAs: key step kk = i / (D / 32), dim block nb
+  constexpr int kQk = 2 * (D / 16);  // K Q^T MFMAs: dim step ks = j / 2, key block j % 2
+  constexpr int kSteps = kPv + kQk;
+  constexpr int kAhead = FL_PP_AHEAD;
+  static_assert(kAhead >= 1 && kAhead <= kPv, "prefetched fragments are V fragments");
+  static_assert(8 * (kDmaPerWave - 1) + 1 < kSteps, "one tile load every 8 MFMAs");
+  auto read_frag = [&](auto slot_tag, auto i_tag) -> u32x4 {
     constexpr int kS = decltype(slot_tag)::value;
-    constexpr int kPv = 4 * (D / 32);  // P V MFMAs: key step kk = i / (D / 32), dim block nb
-    constexpr int kQk = 2 * (D / 16);  // K Q^T MFMAs: dim step ks = j / 2, key block j % 2
-    constexpr int kSteps = kPv + kQk;
-    constexpr int kAhead = FL_PP_AHEAD;
-    const char* vt = lds_bytes + v_slot_offset(std::integral_constant<int, kS + kStages - 1>{});
-    const char* kt = reinterpret_cast<const char*>(k_slot(std::integral_constant<int, kS>{}));
-    auto read_frag = [&](auto i_tag) -> u32x4 {
-      constexpr int i = decltype(i_tag)::value;
-      if constexpr (i < kPv) {
-        constexpr int kk = i / (D / 32), nb = i % (D / 32);
-        return v_frag_at(vt + kk * kKeyStepBytes<D>, v_lds[nb][0], v_lds[nb][1]);
-      } else {
-        constexpr int j = i - kPv, ks = j / 2, blk = j % 2;
-        return lds_load16(kt + blk * kKeyBlockBytes<D>, k_lds[ks]);
-      }
-    };
+    constexpr int i = decltype(i_tag)::value;
+    if constexpr (i < kPv) {
+      constexpr int kk = i / (D / 32), nb = i % (D / 32);
+      const char* vt = lds_bytes + v_slot_offset(std::integral_constant<int, kS + kStages - 1>{});
+      return v_frag_at(vt + kk * kKeyStepBytes<D>, v_lds[nb][0], v_lds[nb][1]);
+    } else {
+      constexpr int j = i - kPv, ks = j / 2, blk = j % 2;
+      const char* kt = reinterpret_cast<const char*>(k_slot(std::integral_constant<int, kS>{}));
+      return lds_load16(kt + blk * kKeyBlockBytes<D>, k_lds[ks]);
+    }
+  };
+  u32x4 fr[kSteps];
+  auto prefetch = [&](auto slot_tag) {
+    static_for<0, kAhead>([&](auto i) { fr[decltype(i)::value] = read_frag(slot_tag, i); });
+  };
+  auto mfma_phase = [&](auto slot_tag, auto&& hook) {
     auto issue = [&](auto i_tag, const u32x4& f) {
       constexpr int i = decltype(i_tag)::value;
       if constexpr (i < kPv) {
@@ -278,38 +301,66 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
         acc = E::mfma32(f, qf[ks], ks == 0 ? f32x16{} : acc);
       }
     };
-#if FL_PP_SETPRIO
+#if FL_PP_SETPRIO == 1
     __builtin_amdgcn_s_setprio(1);
 #endif
-    u32x4 fr[kSteps];
-    static_for<0, kAhead>([&](auto i) { fr[decltype(i)::value] = read_frag(i); });
     __builtin_amdgcn_sched_barrier(0);
     static_for<0, kSteps>([&](auto i) {
       constexpr int n = decltype(i)::value;
       issue(i, fr[n]);
-      if constexpr (n + kAhead < kSteps) fr[n + kAhead] = read_frag(std::integral_constant<int, n + kAhead>{});
+      if constexpr (n + kAhead < kSteps) {
+        fr[n + kAhead] = read_frag(slot_tag, std::integral_constant<int, n + kAhead>{});
+      }
+      hook(i);
       __builtin_amdgcn_sched_barrier(0);
     });
-#if FL_PP_SETPRIO
+#if FL_PP_SETPRIO == 1
     __builtin_amdgcn_s_setprio(0);
 #endif
   };
+  auto no_hook = [](auto) {};
 
-  // Softmax phase for tile t: S(t) -> P(t) (input type, packed as the next P V's B operand), the
-  // lazily moved reference point, the O rescale and the running sum.
-  auto softmax_phase = [&](int t) {
-    if (t < 0 || t >= my_tiles) {
+  // P(t) from S(t) against the reference point: p = 2^(s scale_log2 + neg_shift), packed (rounded
+  // to the input type) as the P V operand; returns the lane's sum of the unrounded probabilities
+  // (fp32 adds: v_dot2 on the packed values would be shorter, but on gfx950 it waits behind the
+  // other wave's MFMAs, which more than doubles the phase).
+  auto probabilities = [&](float neg_shift) -> float {
+    f32x16 p0, p1;
+    float r0 = 0.f;
+    float r1 = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      p0[j] = exp2_fast(fmaf(s0[j], sl2, neg_shift));
+      p1[j] = exp2_fast(fmaf(s1[j], sl2, neg_shift));
+      r0 += p0[j];
+      r1 += p1[j];
+    }
+    pf[0] = p_frag<Tag, 0>(p0);
+    pf[1] = p_frag<Tag, 1>(p0);
+    pf[2] = p_frag<Tag, 0>(p1);
+    pf[3] = p_frag<Tag, 1>(p1);
+    return r0 + r1;
+  };
+
+  // Softmax phase for tile t: S(t) -> P(t) and the running sum. The reference point `ref` (log2
+  // units, the same for both halves of a row) only moves when it must: the probabilities are first
+  // computed against the current one, and only if a lane's sum exceeds kSumLimit (so some p might
+  // leave the comfortable range of the packed operand; fp16 tops out at 65504) does the wave take
+  // the max / rescale path and recompute them. A row without a reference yet (kNoRef) overflows
+  // on its first tile with a visible key. The row max is therefore not needed on most tiles, and
+  // every probability stays <= kSumLimit.
+  auto softmax_body = [&](int t) {
+    if (static_cast<unsigned>(t) >= static_cast<unsigned>(my_tiles)) {
       // This wave sees no key of tile t: the P V that follows must add nothing.
 #pragma unroll
       for (int i = 0; i < 4; ++i) pf[i] = u32x4{0, 0, 0, 0};
       return;
     }
-    const int k0 = t * kBlockN;
-    if ((k0 + kBlockN > a.seqlen_k) || (a.causal && k0 + kBlockN - 1 > row0 + a.causal_offset)) {
+    if (t >= mask_from) {
       asm volatile("" ::: "memory");
       // acc_key(j, half) = acc_key(j, 0) + 4 half: fold the lane's part into the limit so every
       // comparison is against a compile-time constant (no per-key registers live in the loop).
-      const int lim = last_key - k0 - 4 * half;
+      const int lim = last_key - t * kBlockN - 4 * half;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         constexpr int kBase = 0;
@@ -318,71 +369,94 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
         if (kj + 32 > lim) s1[j] = -INFINITY;
       }
     }
-    const float mx = max_halves(max_of(s0, s1));
-    const float cand = mx * sl2;
-    const bool move = cand > ref + kRescaleSlack;
-    const float alpha = move ? exp2_fast(ref - cand) : 1.f;
-    ref = move ? cand : ref;
-    if (wave_any(move)) {
+    float rs = probabilities(-ref);
+    if (wave_any(rs > kSumLimit)) {
       asm volatile("" ::: "memory");
+      const float moved = fmaxf(ref, max_halves(max_of(s0, s1)) * sl2);
+      const float alpha = exp2_fast(ref - moved);
+      ref = moved;
+      if (wave_any(alpha != 1.f)) {
 #pragma unroll
-      for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
+        for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
+      }
+      l *= alpha;
+      rs = probabilities(-ref);
     }
-    const float shift = ref == -INFINITY ? 0.f : ref;
-    float rs0 = 0.f;
-    float rs1 = 0.f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      s0[j] = exp2_fast(fmaf(s0[j], sl2, -shift));
-      s1[j] = exp2_fast(fmaf(s1[j], sl2, -shift));
-      rs0 += s0[j];
-      rs1 += s1[j];
-    }
-    l = fmaf(l, alpha, rs0 + rs1);
-    pf[0] = p_frag<Tag, 0>(s0);
-    pf[1] = p_frag<Tag, 1>(s0);
-    pf[2] = p_frag<Tag, 0>(s1);
-    pf[3] = p_frag<Tag, 1>(s1);
+    l += rs;
+  };
+  auto softmax_phase = [&](int t) {
+#if FL_PP_SETPRIO == 2
+    __builtin_amdgcn_s_setprio(1);
+#endif
+    softmax_body(t);
+#if FL_PP_SETPRIO == 2
+    __builtin_amdgcn_s_setprio(0);
+#endif
   };
 
-  // Vmcnt allowed before the barrier that publishes a batch: the kStages - 2 batches issued after it.
-  constexpr int kLoadsPerBatch = 2 * kDmaPerWave;
-  constexpr int kPendingAfter = (kStages - 2) * kLoadsPerBatch;
+  // Each group waits for its own loads at the end of its softmax phase in period m: group 0 for
+  // K(m + 1) (first read in half-period 2m + 2) with the kStages - 2 later K tiles still in flight,
+  // group 1 for V(m) (first read in half-period 2m + 1) with the kStages - 3 later V tiles.
+  constexpr int kPendingK = (kStages - 2) * kDmaPerWave;
+  constexpr int kPendingV = (kStages - 3) * kDmaPerWave;
 
-  // Prologue: group 1 loads batches 0 .. kStages - 2; batch 0 (K(0)) must be in LDS before the
-  // first half-period.
-  if (group == 1) {
-    load_batch(0, std::integral_constant<int, 0>{}, std::integral_constant<int, kStages - 1>{});
-    if constexpr (kStages > 2) load_batch(1, std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
-    if constexpr (kStages > 3) load_batch(2, std::integral_constant<int, 2>{}, std::integral_constant<int, 1>{});
-    // Loads issued after batch 0: batches 1 .. kStages - 2.
-    wait_vmcnt<(kStages - 2) * kLoadsPerBatch>();
-  }
+  // Prologue: group 0 loads K(0 .. kStages - 2), group 1 V(-1 .. kStages - 3) (V(-1) is zeros, the
+  // P V of period 0); K(0) and V(-1) must be in LDS before the first half-period.
+  static_for<0, kStages - 1>([&](auto i_tag) {
+    constexpr int i = decltype(i_tag)::value;
+    if (group == 0) {
+      load_tile(i, i_tag);
+    } else {
+      load_tile(i - 1, std::integral_constant<int, i + kStages - 1>{});
+    }
+  });
+  wait_vmcnt<(kStages - 2) * kDmaPerWave>();
   phase_barrier();
 
-  // Period m: half-period 2m then 2m + 1. Group 0: MFMA(m), softmax(m). Group 1: softmax(m - 1)
-  // after issuing batch m + kStages - 1, then MFMA(m). Group 1 waits for batch m + 1 before the
-  // barrier that ends half-period 2m (batch m + 1 is first read in half-period 2m + 2). Each group
-  // runs its own straight-line loop, unrolled by kStages so that ring slots are compile-time
-  // immediates; the periods % kStages left over run after it.
+  // Period m: half-period 2m then 2m + 1. Group 0: MFMA(m), softmax(m). Group 1: softmax(m - 1),
+  // then MFMA(m). Each MFMA phase issues its group's next tile between its MFMAs (the descriptor
+  // after MFMA 0, block j after MFMA 8j + 1). Each group runs its own straight-line loop, unrolled
+  // by kStages so that ring slots are compile-time immediates; the periods % kStages left over run
+  // after it.
   const int periods = num_tiles + 1;  // the last one only finishes P V of the last tile
   auto run = [&](auto group_tag) {
     constexpr int kGroup = decltype(group_tag)::value;
     auto period = [&](int m, auto slot_tag) {
       constexpr int kS = decltype(slot_tag)::value;
       if constexpr (kGroup == 0) {
-        mfma_phase(slot_tag);
+        if (m == 0) prefetch(slot_tag);
+        // K(m + kStages - 1) into slot (m - 1) % kStages.
+        u32x4s w;
+        mfma_phase(slot_tag, [&](auto i_tag) {
+          constexpr int i = decltype(i_tag)::value;
+          if constexpr (i == 0) w = tile_words(m + kStages - 1);
+          if constexpr (i % 8 == 1 && i / 8 < kDmaPerWave) {
+            issue_block(w, std::integral_constant<int, kS + kStages - 1>{},
+                        std::integral_constant<int, i / 8>{});
+          }
+        });
         phase_barrier();
+        // The next MFMA phase's first fragments (V(m), published by the barrier that ended
+        // half-period 2m), read first so their latency hides behind the softmax.
+        prefetch(std::integral_constant<int, kS + 1>{});
         softmax_phase(m);
+        wait_vmcnt<kPendingK>();  // K(m + 1), first read in half-period 2m + 2
         phase_barrier();
       } else {
-        // Batch m + kStages - 1: K into slot (m - 1) % kStages, V into slot (m - 2) % kStages.
-        load_batch(m + kStages - 1, std::integral_constant<int, kS + kStages - 1>{},
-                   std::integral_constant<int, kS + kStages - 2>{});
+        prefetch(slot_tag);
         softmax_phase(m - 1);
-        wait_vmcnt<kPendingAfter>();
+        wait_vmcnt<kPendingV>();  // V(m), first read in half-period 2m + 1
         phase_barrier();
-        mfma_phase(slot_tag);
+        // V(m + kStages - 2) into slot (m - 2) % kStages.
+        u32x4s w;
+        mfma_phase(slot_tag, [&](auto i_tag) {
+          constexpr int i = decltype(i_tag)::value;
+          if constexpr (i == 0) w = tile_words(m + kStages - 2);
+          if constexpr (i % 8 == 1 && i / 8 < kDmaPerWave) {
+            issue_block(w, std::integral_constant<int, kS + kStages - 2>{},
+                        std::integral_constant<int, i / 8>{});
+          }
+        });
         phase_barrier();
       }
     };
@@ -390,7 +464,7 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     for (; m + kStages <= periods; m += kStages) {
       period(m, std::integral_constant<int, 0>{});
       period(m + 1, std::integral_constant<int, 1>{});
-      if constexpr (kStages > 2) period(m + 2, std::integral_constant<int, 2>{});
+      period(m + 2, std::integral_constant<int, 2>{});
       if constexpr (kStages > 3) period(m + 3, std::integral_constant<int, 3>{});
     }
     const int rest = periods - m;
@@ -407,7 +481,7 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   }
   // Loads past the end may still be in flight into free slots; they must land before the
   // workgroup's LDS is handed to another workgroup.
-  if (group == 1) wait_vmcnt<0>();
+  wait_vmcnt<0>();
 
   const float lt = sum_halves(l);
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
