@@ -123,9 +123,16 @@ __device__ __forceinline__ u32x4s buffer_words(const void* base, uint32_t bytes)
 }
 __device__ __forceinline__ void buffer_load16_to_lds_asm(u32x4s words, uint32_t lds_addr,
                                                          int offset) {
+  // The address and resource are wave-uniform by contract; readfirstlane makes that explicit to
+  // the compiler so they are always given scalar registers (a no-op when they already are).
+  auto uniform = [](uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x)));
+  };
+  const u32x4s w{uniform(words[0]), uniform(words[1]), uniform(words[2]), uniform(words[3])};
+  const uint32_t m0 = uniform(lds_addr);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
                :
-               : "v"(offset), "s"(lds_addr), "s"(words)
+               : "v"(offset), "s"(m0), "s"(w)
                : "memory", "m0");
 }
 // 32-bit LDS address of a __shared__ object.

@@ -29,8 +29,8 @@
 //    they are first read. Loads past the last tile use an empty buffer resource (they write zeros
 //    into a free slot) so every wave issues the same number of loads and the vmcnt accounting is
 //    uniform.
-//  * Work order as in prefill_fwd.hip: XCD-contiguous (batch, head) ranges; causal query blocks
-//    heaviest first.
+//  * Work order: XCD-contiguous (batch, head) ranges (workgroups are dealt round-robin over the 8
+//    XCDs, each with its own L2); causal query blocks in heavy/light pairs per workgroup.
 #include <type_traits>
 
 #include "launch.hpp"
@@ -149,47 +149,20 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   const int group = wave >> 2;
   const int half = lane >> 5;
 
+  // Work item: (batch, head) and query blocks. Non-causal: one block per workgroup. Causal: the
+  // blocks of a (batch, head) go in pairs (q_blocks - 1 - i, i), heavy first, so every workgroup
+  // runs about the same number of tiles (a plain heaviest-first order still leaves a tail of heavy
+  // blocks dealt late) and the light block's K and V are a prefix of the heavy one's.
   const int work = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = work / a.q_blocks;
-  int qb = work - bh * a.q_blocks;
-  if (a.causal) qb = a.q_blocks - 1 - qb;
+  const int items_per_bh = a.causal ? (a.q_blocks + 1) / 2 : a.q_blocks;
+  const int bh = work / items_per_bh;
+  const int item = work - bh * items_per_bh;
   const int b = bh / a.heads;
   const int h = bh - b * a.heads;
   const int hkv = h / a.group;
-  const int q0 = qb * kPpBlockM;
-  const int row0 = q0 + wave * kRowsPerWave;
-  const int my_row = row0 + (lane & 31);
-
   const uint16_t* qp = a.q + b * a.q_bs + h * a.q_hs;
   const uint16_t* kp = a.k + b * a.k_bs + hkv * a.k_hs;
   const uint16_t* vp = a.v + b * a.v_bs + hkv * a.v_hs;
-
-  int kv_end = a.seqlen_k;
-  if (a.causal) kv_end = min(kv_end, min(q0 + kPpBlockM, a.seqlen_q) + a.causal_offset);
-  const int num_tiles = kv_end > 0 ? (kv_end + kBlockN - 1) / kBlockN : 0;
-  // Tiles this wave sees any key of (a prefix of the workgroup's tiles), and the first tile whose
-  // scores need masking (it reaches past the sequence end or, causal, past the diagonal of the
-  // wave's first row): every tile before it is fully visible to every row of the wave.
-  int my_tiles = num_tiles;
-  int mask_from = a.seqlen_k / kBlockN;
-  if (a.causal) {
-    const int last = row0 + kRowsPerWave - 1 + a.causal_offset;  // last key any of its rows sees
-    my_tiles = last < 0 ? 0 : min(num_tiles, last / kBlockN + 1);
-    const int x = row0 + a.causal_offset - (kBlockN - 1);  // tile t needs masking iff 64 t > x
-    mask_from = min(mask_from, x < 0 ? 0 : x / kBlockN + 1);
-  }
-
-  u32x4 qf[D / 16];
-  {
-    const bool ok = my_row < a.seqlen_q;
-    const uint16_t* src = qp + static_cast<int64_t>(ok ? my_row : 0) * a.q_ss + 8 * half;
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) qf[ks] = ok ? load16(src + 16 * ks) : u32x4{0, 0, 0, 0};
-    // Consume the Q registers here so the compiler's wait for them sits before the tile loads
-    // (it does not see those, and would otherwise wait for all of them at the first use of Q).
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) asm volatile("" : "+v"(qf[ks]));
-  }
 
   int k_lds[D / 16];
 #pragma unroll
@@ -226,288 +199,332 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   // valid rows (full tiles before the last one, the last one up to the sequence end, none outside
   // [0, num_tiles): those read as zeros).
   const int64_t tile_bytes = static_cast<int64_t>(kBlockN) * my_ss * 2;
-  const int last_rows = num_tiles > 0 ? min(kBlockN, a.seqlen_k - (num_tiles - 1) * kBlockN) : 1;
-  const uint32_t full_bytes = static_cast<uint32_t>(((kBlockN - 1) * my_ss + D) * 2);
-  const uint32_t last_bytes = static_cast<uint32_t>(((last_rows - 1) * my_ss + D) * 2);
-  auto tile_words = [&](int t) -> u32x4s {
-    const bool inside = t >= 0 && t < num_tiles;
-    const uint32_t bytes = !inside ? 0u : t == num_tiles - 1 ? last_bytes : full_bytes;
-    const char* p = reinterpret_cast<const char*>(my_base) + (inside ? t * tile_bytes : 0);
-    return buffer_words(p, bytes);
-  };
-  // Block j of the group's tile (descriptor `w`) into ring slot kSlot.
-  auto issue_block = [&](u32x4s w, auto slot_tag, auto j_tag) {
-    constexpr int j = decltype(j_tag)::value;
-    constexpr uint32_t kOff = (decltype(slot_tag)::value % kStages) * kSlotBytes + j * 1024;
-    buffer_load16_to_lds_asm(w, lds_wave + kOff, my_off[j]);
-  };
-  auto load_tile = [&](int t, auto slot_tag) {
-    const u32x4s w = tile_words(t);
-    static_for<0, kDmaPerWave>([&](auto j) { issue_block(w, slot_tag, j); });
-  };
+  // One query block of kPpBlockM rows: its own tile range, pipeline and epilogue. Every wave has
+  // finished with the LDS ring and every tile load has landed when it returns.
+  auto process = [&](const int qb) {
+    const int q0 = qb * kPpBlockM;
+    const int row0 = q0 + wave * kRowsPerWave;
+    const int my_row = row0 + (lane & 31);
 
-  f32x16 o[D / 32];
-#pragma unroll
-  for (int nb = 0; nb < D / 32; ++nb) o[nb] = f32x16{};
-  f32x16 s0 = f32x16{};
-  f32x16 s1 = f32x16{};
-  u32x4 pf[4] = {};
-  float ref = kNoRef;
-  float l = 0.f;
-  const float sl2 = a.scale_log2;
-  const int last_key = a.causal ? min(a.seqlen_k - 1, my_row + a.causal_offset) : a.seqlen_k - 1;
-
-  // MFMA phase of a period with slots kS = m % kStages: O += V(m-1) P(m-1) (16 MFMAs), then
-  // S = K(m) Q^T (16 MFMAs). No branches: in period 0 the previous P and V are zeros (P starts at
-  // 0, the V slot was filled from an empty resource), a skipped softmax leaves P = 0, and scores of
-  // tiles nobody reads are never used. The 32 MFMAs form one software pipeline: the A-operand
-  // fragment of MFMA i + kAhead is read from LDS right after MFMA i issues, and a scheduling
-  // barrier after every step keeps that order (left to itself the scheduler reads each fragment
-  // just before its MFMA and the LDS latency shows on every step). The first kAhead fragments are
-  // read at the end of the wave's softmax phase (prefetch), so the MFMA phase starts without
-  // waiting for LDS. hook(i) runs after MFMA i (the tile loads are issued there).
-  constexpr int kPv = 4 * (D / 32);  // P V MFMAs: key step kk = i / (D / 32), dim block nb
-  constexpr int kQk = 2 * (D / 16);  // K Q^T MFMAs: dim step ks = j / 2, key block j % 2
-  constexpr int kSteps = kPv + kQk;
-  constexpr int kAhead = FL_PP_AHEAD;
-  static_assert(kAhead >= 1 && kAhead <= kPv, "prefetched fragments are V fragments");
-  static_assert(8 * (kDmaPerWave - 1) + 1 < kSteps, "one tile load every 8 MFMAs");
-  auto read_frag = [&](auto slot_tag, auto i_tag) -> u32x4 {
-    constexpr int kS = decltype(slot_tag)::value;
-    constexpr int i = decltype(i_tag)::value;
-    if constexpr (i < kPv) {
-      constexpr int kk = i / (D / 32), nb = i % (D / 32);
-      const char* vt = lds_bytes + v_slot_offset(std::integral_constant<int, kS + kStages - 1>{});
-      return v_frag_at(vt + kk * kKeyStepBytes<D>, v_lds[nb][0], v_lds[nb][1]);
-    } else {
-      constexpr int j = i - kPv, ks = j / 2, blk = j % 2;
-      const char* kt = reinterpret_cast<const char*>(k_slot(std::integral_constant<int, kS>{}));
-      return lds_load16(kt + blk * kKeyBlockBytes<D>, k_lds[ks]);
+    int kv_end = a.seqlen_k;
+    if (a.causal) kv_end = min(kv_end, min(q0 + kPpBlockM, a.seqlen_q) + a.causal_offset);
+    const int num_tiles = kv_end > 0 ? (kv_end + kBlockN - 1) / kBlockN : 0;
+    // Tiles this wave sees any key of (a prefix of the workgroup's tiles), and the first tile whose
+    // scores need masking (it reaches past the sequence end or, causal, past the diagonal of the
+    // wave's first row): every tile before it is fully visible to every row of the wave.
+    int my_tiles = num_tiles;
+    int mask_from = a.seqlen_k / kBlockN;
+    if (a.causal) {
+      const int last = row0 + kRowsPerWave - 1 + a.causal_offset;  // last key any of its rows sees
+      my_tiles = last < 0 ? 0 : min(num_tiles, last / kBlockN + 1);
+      const int x = row0 + a.causal_offset - (kBlockN - 1);  // tile t needs masking iff 64 t > x
+      mask_from = min(mask_from, x < 0 ? 0 : x / kBlockN + 1);
     }
-  };
-  u32x4 fr[kSteps];
-  auto prefetch = [&](auto slot_tag) {
-    static_for<0, kAhead>([&](auto i) { fr[decltype(i)::value] = read_frag(slot_tag, i); });
-  };
-  auto mfma_phase = [&](auto slot_tag, auto&& hook) {
-    auto issue = [&](auto i_tag, const u32x4& f) {
+
+    u32x4 qf[D / 16];
+    {
+      const bool ok = my_row < a.seqlen_q;
+      const uint16_t* src = qp + static_cast<int64_t>(ok ? my_row : 0) * a.q_ss + 8 * half;
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks) qf[ks] = ok ? load16(src + 16 * ks) : u32x4{0, 0, 0, 0};
+      // Consume the Q registers here so the compiler's wait for them sits before the tile loads
+      // (it does not see those, and would otherwise wait for all of them at the first use of Q).
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks) asm volatile("" : "+v"(qf[ks]));
+    }
+
+    const int last_rows = num_tiles > 0 ? min(kBlockN, a.seqlen_k - (num_tiles - 1) * kBlockN) : 1;
+    const uint32_t full_bytes = static_cast<uint32_t>(((kBlockN - 1) * my_ss + D) * 2);
+    const uint32_t last_bytes = static_cast<uint32_t>(((last_rows - 1) * my_ss + D) * 2);
+    auto tile_words = [&](int t) -> u32x4s {
+      const bool inside = t >= 0 && t < num_tiles;
+      const uint32_t bytes = !inside ? 0u : t == num_tiles - 1 ? last_bytes : full_bytes;
+      const char* p = reinterpret_cast<const char*>(my_base) + (inside ? t * tile_bytes : 0);
+      return buffer_words(p, bytes);
+    };
+    // Block j of the group's tile (descriptor `w`) into ring slot kSlot.
+    auto issue_block = [&](u32x4s w, auto slot_tag, auto j_tag) {
+      constexpr int j = decltype(j_tag)::value;
+      constexpr uint32_t kOff = (decltype(slot_tag)::value % kStages) * kSlotBytes + j * 1024;
+      buffer_load16_to_lds_asm(w, lds_wave + kOff, my_off[j]);
+    };
+    auto load_tile = [&](int t, auto slot_tag) {
+      const u32x4s w = tile_words(t);
+      static_for<0, kDmaPerWave>([&](auto j) { issue_block(w, slot_tag, j); });
+    };
+
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int nb = 0; nb < D / 32; ++nb) o[nb] = f32x16{};
+    f32x16 s0 = f32x16{};
+    f32x16 s1 = f32x16{};
+    u32x4 pf[4] = {};
+    float ref = kNoRef;
+    float l = 0.f;
+    const float sl2 = a.scale_log2;
+    const int last_key = a.causal ? min(a.seqlen_k - 1, my_row + a.causal_offset) : a.seqlen_k - 1;
+
+    // MFMA phase of a period with slots kS = m % kStages: O += V(m-1) P(m-1) (16 MFMAs), then
+    // S = K(m) Q^T (16 MFMAs). No branches: in period 0 the previous P and V are zeros (P starts at
+    // 0, the V slot was filled from an empty resource), a skipped softmax leaves P = 0, and scores of
+    // tiles nobody reads are never used. The 32 MFMAs form one software pipeline: the A-operand
+    // fragment of MFMA i + kAhead is read from LDS right after MFMA i issues, and a scheduling
+    // barrier after every step keeps that order (left to itself the scheduler reads each fragment
+    // just before its MFMA and the LDS latency shows on every step). The first kAhead fragments are
+    // read at the end of the wave's softmax phase (prefetch), so the MFMA phase starts without
+    // waiting for LDS. hook(i) runs after MFMA i (the tile loads are issued there).
+    constexpr int kPv = 4 * (D / 32);  // P V MFMAs: key step kk = i / (D / 32), dim block nb
+    constexpr int kQk = 2 * (D / 16);  // K Q^T MFMAs: dim step ks = j / 2, key block j % 2
+    constexpr int kSteps = kPv + kQk;
+    constexpr int kAhead = FL_PP_AHEAD;
+    static_assert(kAhead >= 1 && kAhead <= kPv, "prefetched fragments are V fragments");
+    static_assert(8 * (kDmaPerWave - 1) + 1 < kSteps, "one tile load every 8 MFMAs");
+    auto read_frag = [&](auto slot_tag, auto i_tag) -> u32x4 {
+      constexpr int kS = decltype(slot_tag)::value;
       constexpr int i = decltype(i_tag)::value;
       if constexpr (i < kPv) {
         constexpr int kk = i / (D / 32), nb = i % (D / 32);
-        o[nb] = E::mfma32(f, pf[kk], o[nb]);
+        const char* vt = lds_bytes + v_slot_offset(std::integral_constant<int, kS + kStages - 1>{});
+        return v_frag_at(vt + kk * kKeyStepBytes<D>, v_lds[nb][0], v_lds[nb][1]);
       } else {
         constexpr int j = i - kPv, ks = j / 2, blk = j % 2;
-        f32x16& acc = blk == 0 ? s0 : s1;
-        acc = E::mfma32(f, qf[ks], ks == 0 ? f32x16{} : acc);
+        const char* kt = reinterpret_cast<const char*>(k_slot(std::integral_constant<int, kS>{}));
+        return lds_load16(kt + blk * kKeyBlockBytes<D>, k_lds[ks]);
       }
     };
+    u32x4 fr[kSteps];
+    auto prefetch = [&](auto slot_tag) {
+      static_for<0, kAhead>([&](auto i) { fr[decltype(i)::value] = read_frag(slot_tag, i); });
+    };
+    auto mfma_phase = [&](auto slot_tag, auto&& hook) {
+      auto issue = [&](auto i_tag, const u32x4& f) {
+        constexpr int i = decltype(i_tag)::value;
+        if constexpr (i < kPv) {
+          constexpr int kk = i / (D / 32), nb = i % (D / 32);
+          o[nb] = E::mfma32(f, pf[kk], o[nb]);
+        } else {
+          constexpr int j = i - kPv, ks = j / 2, blk = j % 2;
+          f32x16& acc = blk == 0 ? s0 : s1;
+          acc = E::mfma32(f, qf[ks], ks == 0 ? f32x16{} : acc);
+        }
+      };
 #if FL_PP_SETPRIO == 1
-    __builtin_amdgcn_s_setprio(1);
+      __builtin_amdgcn_s_setprio(1);
 #endif
-    __builtin_amdgcn_sched_barrier(0);
-    static_for<0, kSteps>([&](auto i) {
-      constexpr int n = decltype(i)::value;
-      issue(i, fr[n]);
-      if constexpr (n + kAhead < kSteps) {
-        fr[n + kAhead] = read_frag(slot_tag, std::integral_constant<int, n + kAhead>{});
-      }
-      hook(i);
       __builtin_amdgcn_sched_barrier(0);
-    });
+      static_for<0, kSteps>([&](auto i) {
+        constexpr int n = decltype(i)::value;
+        issue(i, fr[n]);
+        if constexpr (n + kAhead < kSteps) {
+          fr[n + kAhead] = read_frag(slot_tag, std::integral_constant<int, n + kAhead>{});
+        }
+        hook(i);
+        __builtin_amdgcn_sched_barrier(0);
+      });
 #if FL_PP_SETPRIO == 1
-    __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_s_setprio(0);
 #endif
-  };
-  auto no_hook = [](auto) {};
+    };
+    auto no_hook = [](auto) {};
 
-  // P(t) from S(t) against the reference point: p = 2^(s scale_log2 + neg_shift), packed (rounded
-  // to the input type) as the P V operand; returns the lane's sum of the unrounded probabilities
-  // (fp32 adds: v_dot2 on the packed values would be shorter, but on gfx950 it waits behind the
-  // other wave's MFMAs, which more than doubles the phase).
-  auto probabilities = [&](float neg_shift) -> float {
-    f32x16 p0, p1;
-    float r0 = 0.f;
-    float r1 = 0.f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      p0[j] = exp2_fast(fmaf(s0[j], sl2, neg_shift));
-      p1[j] = exp2_fast(fmaf(s1[j], sl2, neg_shift));
-      r0 += p0[j];
-      r1 += p1[j];
-    }
-    pf[0] = p_frag<Tag, 0>(p0);
-    pf[1] = p_frag<Tag, 1>(p0);
-    pf[2] = p_frag<Tag, 0>(p1);
-    pf[3] = p_frag<Tag, 1>(p1);
-    return r0 + r1;
-  };
-
-  // Softmax phase for tile t: S(t) -> P(t) and the running sum. The reference point `ref` (log2
-  // units, the same for both halves of a row) only moves when it must: the probabilities are first
-  // computed against the current one, and only if a lane's sum exceeds kSumLimit (so some p might
-  // leave the comfortable range of the packed operand; fp16 tops out at 65504) does the wave take
-  // the max / rescale path and recompute them. A row without a reference yet (kNoRef) overflows
-  // on its first tile with a visible key. The row max is therefore not needed on most tiles, and
-  // every probability stays <= kSumLimit.
-  auto softmax_body = [&](int t) {
-    if (static_cast<unsigned>(t) >= static_cast<unsigned>(my_tiles)) {
-      // This wave sees no key of tile t: the P V that follows must add nothing.
-#pragma unroll
-      for (int i = 0; i < 4; ++i) pf[i] = u32x4{0, 0, 0, 0};
-      return;
-    }
-    if (t >= mask_from) {
-      asm volatile("" ::: "memory");
-      // acc_key(j, half) = acc_key(j, 0) + 4 half: fold the lane's part into the limit so every
-      // comparison is against a compile-time constant (no per-key registers live in the loop).
-      const int lim = last_key - t * kBlockN - 4 * half;
+    // P(t) from S(t) against the reference point: p = 2^(s scale_log2 + neg_shift), packed (rounded
+    // to the input type) as the P V operand; returns the lane's sum of the unrounded probabilities
+    // (fp32 adds: v_dot2 on the packed values would be shorter, but on gfx950 it waits behind the
+    // other wave's MFMAs, which more than doubles the phase).
+    auto probabilities = [&](float neg_shift) -> float {
+      f32x16 p0, p1;
+      float r0 = 0.f;
+      float r1 = 0.f;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        constexpr int kBase = 0;
-        const int kj = acc_key(j, kBase);
-        if (kj > lim) s0[j] = -INFINITY;
-        if (kj + 32 > lim) s1[j] = -INFINITY;
+        p0[j] = exp2_fast(fmaf(s0[j], sl2, neg_shift));
+        p1[j] = exp2_fast(fmaf(s1[j], sl2, neg_shift));
+        r0 += p0[j];
+        r1 += p1[j];
       }
-    }
-    float rs = probabilities(-ref);
-    if (wave_any(rs > kSumLimit)) {
-      asm volatile("" ::: "memory");
-      const float moved = fmaxf(ref, max_halves(max_of(s0, s1)) * sl2);
-      const float alpha = exp2_fast(ref - moved);
-      ref = moved;
-      if (wave_any(alpha != 1.f)) {
+      pf[0] = p_frag<Tag, 0>(p0);
+      pf[1] = p_frag<Tag, 1>(p0);
+      pf[2] = p_frag<Tag, 0>(p1);
+      pf[3] = p_frag<Tag, 1>(p1);
+      return r0 + r1;
+    };
+
+    // Softmax phase for tile t: S(t) -> P(t) and the running sum. The reference point `ref` (log2
+    // units, the same for both halves of a row) only moves when it must: the probabilities are first
+    // computed against the current one, and only if a lane's sum exceeds kSumLimit (so some p might
+    // leave the comfortable range of the packed operand; fp16 tops out at 65504) does the wave take
+    // the max / rescale path and recompute them. A row without a reference yet (kNoRef) overflows
+    // on its first tile with a visible key. The row max is therefore not needed on most tiles, and
+    // every probability stays <= kSumLimit.
+    auto softmax_body = [&](int t) {
+      if (static_cast<unsigned>(t) >= static_cast<unsigned>(my_tiles)) {
+        // This wave sees no key of tile t: the P V that follows must add nothing.
 #pragma unroll
-        for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
+        for (int i = 0; i < 4; ++i) pf[i] = u32x4{0, 0, 0, 0};
+        return;
       }
-      l *= alpha;
-      rs = probabilities(-ref);
-    }
-    l += rs;
-  };
-  auto softmax_phase = [&](int t) {
+      if (t >= mask_from) {
+        asm volatile("" ::: "memory");
+        // acc_key(j, half) = acc_key(j, 0) + 4 half: fold the lane's part into the limit so every
+        // comparison is against a compile-time constant (no per-key registers live in the loop).
+        const int lim = last_key - t * kBlockN - 4 * half;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          constexpr int kBase = 0;
+          const int kj = acc_key(j, kBase);
+          if (kj > lim) s0[j] = -INFINITY;
+          if (kj + 32 > lim) s1[j] = -INFINITY;
+        }
+      }
+      float rs = probabilities(-ref);
+      if (wave_any(rs > kSumLimit)) {
+        asm volatile("" ::: "memory");
+        const float moved = fmaxf(ref, max_halves(max_of(s0, s1)) * sl2);
+        const float alpha = exp2_fast(ref - moved);
+        ref = moved;
+        if (wave_any(alpha != 1.f)) {
+#pragma unroll
+          for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
+        }
+        l *= alpha;
+        rs = probabilities(-ref);
+      }
+      l += rs;
+    };
+    auto softmax_phase = [&](int t) {
 #if FL_PP_SETPRIO == 2
-    __builtin_amdgcn_s_setprio(1);
+      __builtin_amdgcn_s_setprio(1);
 #endif
-    softmax_body(t);
+      softmax_body(t);
 #if FL_PP_SETPRIO == 2
-    __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_s_setprio(0);
 #endif
-  };
+    };
 
-  // Each group waits for its own loads at the end of its softmax phase in period m: group 0 for
-  // K(m + 1) (first read in half-period 2m + 2) with the kStages - 2 later K tiles still in flight,
-  // group 1 for V(m) (first read in half-period 2m + 1) with the kStages - 3 later V tiles.
-  constexpr int kPendingK = (kStages - 2) * kDmaPerWave;
-  constexpr int kPendingV = (kStages - 3) * kDmaPerWave;
+    // Each group waits for its own loads at the end of its softmax phase in period m: group 0 for
+    // K(m + 1) (first read in half-period 2m + 2) with the kStages - 2 later K tiles still in flight,
+    // group 1 for V(m) (first read in half-period 2m + 1) with the kStages - 3 later V tiles.
+    constexpr int kPendingK = (kStages - 2) * kDmaPerWave;
+    constexpr int kPendingV = (kStages - 3) * kDmaPerWave;
 
-  // Prologue: group 0 loads K(0 .. kStages - 2), group 1 V(-1 .. kStages - 3) (V(-1) is zeros, the
-  // P V of period 0); K(0) and V(-1) must be in LDS before the first half-period.
-  static_for<0, kStages - 1>([&](auto i_tag) {
-    constexpr int i = decltype(i_tag)::value;
-    if (group == 0) {
-      load_tile(i, i_tag);
-    } else {
-      load_tile(i - 1, std::integral_constant<int, i + kStages - 1>{});
-    }
-  });
-  wait_vmcnt<(kStages - 2) * kDmaPerWave>();
-  phase_barrier();
-
-  // Period m: half-period 2m then 2m + 1. Group 0: MFMA(m), softmax(m). Group 1: softmax(m - 1),
-  // then MFMA(m). Each MFMA phase issues its group's next tile between its MFMAs (the descriptor
-  // after MFMA 0, block j after MFMA 8j + 1). Each group runs its own straight-line loop, unrolled
-  // by kStages so that ring slots are compile-time immediates; the periods % kStages left over run
-  // after it.
-  const int periods = num_tiles + 1;  // the last one only finishes P V of the last tile
-  auto run = [&](auto group_tag) {
-    constexpr int kGroup = decltype(group_tag)::value;
-    auto period = [&](int m, auto slot_tag) {
-      constexpr int kS = decltype(slot_tag)::value;
-      if constexpr (kGroup == 0) {
-        if (m == 0) prefetch(slot_tag);
-        // K(m + kStages - 1) into slot (m - 1) % kStages.
-        u32x4s w;
-        mfma_phase(slot_tag, [&](auto i_tag) {
-          constexpr int i = decltype(i_tag)::value;
-          if constexpr (i == 0) w = tile_words(m + kStages - 1);
-          if constexpr (i % 8 == 1 && i / 8 < kDmaPerWave) {
-            issue_block(w, std::integral_constant<int, kS + kStages - 1>{},
-                        std::integral_constant<int, i / 8>{});
-          }
-        });
-        phase_barrier();
-        // The next MFMA phase's first fragments (V(m), published by the barrier that ended
-        // half-period 2m), read first so their latency hides behind the softmax.
-        prefetch(std::integral_constant<int, kS + 1>{});
-        softmax_phase(m);
-        wait_vmcnt<kPendingK>();  // K(m + 1), first read in half-period 2m + 2
-        phase_barrier();
+    // Prologue: group 0 loads K(0 .. kStages - 2), group 1 V(-1 .. kStages - 3) (V(-1) is zeros, the
+    // P V of period 0); K(0) and V(-1) must be in LDS before the first half-period.
+    static_for<0, kStages - 1>([&](auto i_tag) {
+      constexpr int i = decltype(i_tag)::value;
+      if (group == 0) {
+        load_tile(i, i_tag);
       } else {
-        prefetch(slot_tag);
-        softmax_phase(m - 1);
-        wait_vmcnt<kPendingV>();  // V(m), first read in half-period 2m + 1
-        phase_barrier();
-        // V(m + kStages - 2) into slot (m - 2) % kStages.
-        u32x4s w;
-        mfma_phase(slot_tag, [&](auto i_tag) {
-          constexpr int i = decltype(i_tag)::value;
-          if constexpr (i == 0) w = tile_words(m + kStages - 2);
-          if constexpr (i % 8 == 1 && i / 8 < kDmaPerWave) {
-            issue_block(w, std::integral_constant<int, kS + kStages - 2>{},
-                        std::integral_constant<int, i / 8>{});
-          }
-        });
-        phase_barrier();
+        load_tile(i - 1, std::integral_constant<int, i + kStages - 1>{});
+      }
+    });
+    wait_vmcnt<(kStages - 2) * kDmaPerWave>();
+    phase_barrier();
+
+    // Period m: half-period 2m then 2m + 1. Group 0: MFMA(m), softmax(m). Group 1: softmax(m - 1),
+    // then MFMA(m). Each MFMA phase issues its group's next tile between its MFMAs (the descriptor
+    // after MFMA 0, block j after MFMA 8j + 1). Each group runs its own straight-line loop, unrolled
+    // by kStages so that ring slots are compile-time immediates; the periods % kStages left over run
+    // after it.
+    const int periods = num_tiles + 1;  // the last one only finishes P V of the last tile
+    auto run = [&](auto group_tag) {
+      constexpr int kGroup = decltype(group_tag)::value;
+      auto period = [&](int m, auto slot_tag) {
+        constexpr int kS = decltype(slot_tag)::value;
+        if constexpr (kGroup == 0) {
+          if (m == 0) prefetch(slot_tag);
+          // K(m + kStages - 1) into slot (m - 1) % kStages.
+          u32x4s w;
+          mfma_phase(slot_tag, [&](auto i_tag) {
+            constexpr int i = decltype(i_tag)::value;
+            if constexpr (i == 0) w = tile_words(m + kStages - 1);
+            if constexpr (i % 8 == 1 && i / 8 < kDmaPerWave) {
+              issue_block(w, std::integral_constant<int, kS + kStages - 1>{},
+                          std::integral_constant<int, i / 8>{});
+            }
+          });
+          phase_barrier();
+          // The next MFMA phase's first fragments (V(m), published by the barrier that ended
+          // half-period 2m), read first so their latency hides behind the softmax.
+          prefetch(std::integral_constant<int, kS + 1>{});
+          softmax_phase(m);
+          wait_vmcnt<kPendingK>();  // K(m + 1), first read in half-period 2m + 2
+          phase_barrier();
+        } else {
+          prefetch(slot_tag);
+          softmax_phase(m - 1);
+          wait_vmcnt<kPendingV>();  // V(m), first read in half-period 2m + 1
+          phase_barrier();
+          // V(m + kStages - 2) into slot (m - 2) % kStages.
+          u32x4s w;
+          mfma_phase(slot_tag, [&](auto i_tag) {
+            constexpr int i = decltype(i_tag)::value;
+            if constexpr (i == 0) w = tile_words(m + kStages - 2);
+            if constexpr (i % 8 == 1 && i / 8 < kDmaPerWave) {
+              issue_block(w, std::integral_constant<int, kS + kStages - 2>{},
+                          std::integral_constant<int, i / 8>{});
+            }
+          });
+          phase_barrier();
+        }
+      };
+      int m = 0;
+      for (; m + kStages <= periods; m += kStages) {
+        period(m, std::integral_constant<int, 0>{});
+        period(m + 1, std::integral_constant<int, 1>{});
+        period(m + 2, std::integral_constant<int, 2>{});
+        if constexpr (kStages > 3) period(m + 3, std::integral_constant<int, 3>{});
+      }
+      const int rest = periods - m;
+      if (rest > 0) period(m, std::integral_constant<int, 0>{});
+      if (rest > 1) period(m + 1, std::integral_constant<int, 1>{});
+      if constexpr (kStages > 3) {
+        if (rest > 2) period(m + 2, std::integral_constant<int, 2>{});
       }
     };
-    int m = 0;
-    for (; m + kStages <= periods; m += kStages) {
-      period(m, std::integral_constant<int, 0>{});
-      period(m + 1, std::integral_constant<int, 1>{});
-      period(m + 2, std::integral_constant<int, 2>{});
-      if constexpr (kStages > 3) period(m + 3, std::integral_constant<int, 3>{});
+    if (group == 0) {
+      run(std::integral_constant<int, 0>{});
+    } else {
+      run(std::integral_constant<int, 1>{});
     }
-    const int rest = periods - m;
-    if (rest > 0) period(m, std::integral_constant<int, 0>{});
-    if (rest > 1) period(m + 1, std::integral_constant<int, 1>{});
-    if constexpr (kStages > 3) {
-      if (rest > 2) period(m + 2, std::integral_constant<int, 2>{});
-    }
-  };
-  if (group == 0) {
-    run(std::integral_constant<int, 0>{});
-  } else {
-    run(std::integral_constant<int, 1>{});
-  }
-  // Loads past the end may still be in flight into free slots; they must land before the
-  // workgroup's LDS is handed to another workgroup.
-  wait_vmcnt<0>();
+    // Loads past the end may still be in flight into free slots; they must land before the
+    // workgroup's LDS is handed to another workgroup.
+    wait_vmcnt<0>();
 
-  const float lt = sum_halves(l);
-  const float inv = lt > 0.f ? 1.f / lt : 0.f;
-  if (my_row < a.seqlen_q) {
-    uint16_t* orow = a.o + b * a.o_bs + static_cast<int64_t>(my_row) * a.o_ss + h * a.o_hs;
+    const float lt = sum_halves(l);
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    if (my_row < a.seqlen_q) {
+      uint16_t* orow = a.o + b * a.o_bs + static_cast<int64_t>(my_row) * a.o_ss + h * a.o_hs;
 #pragma unroll
-    for (int nb = 0; nb < D / 32; ++nb) {
+      for (int nb = 0; nb < D / 32; ++nb) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d = 32 * nb + 8 * g + 4 * half;
-        const u32x2 packed{E::pack2(o[nb][4 * g] * inv, o[nb][4 * g + 1] * inv),
-                           E::pack2(o[nb][4 * g + 2] * inv, o[nb][4 * g + 3] * inv)};
-        *reinterpret_cast<u32x2*>(orow + d) = packed;
+        for (int g = 0; g < 4; ++g) {
+          const int d = 32 * nb + 8 * g + 4 * half;
+          const u32x2 packed{E::pack2(o[nb][4 * g] * inv, o[nb][4 * g + 1] * inv),
+                             E::pack2(o[nb][4 * g + 2] * inv, o[nb][4 * g + 3] * inv)};
+          *reinterpret_cast<u32x2*>(orow + d) = packed;
+        }
+      }
+      if (half == 0) {
+        a.lse[(static_cast<int64_t>(b) * a.heads + h) * a.seqlen_q + my_row] =
+            lt > 0.f ? ref * kLn2 + logf(lt) : -INFINITY;
       }
     }
-    if (half == 0) {
-      a.lse[(static_cast<int64_t>(b) * a.heads + h) * a.seqlen_q + my_row] =
-          lt > 0.f ? ref * kLn2 + logf(lt) : -INFINITY;
-    }
+  };
+
+  // One call site (a loop), so the block body is inlined once.
+  const int heavy = a.q_blocks - 1 - item;
+  const int blocks_here = a.causal && item < heavy ? 2 : 1;
+  for (int i = 0; i < blocks_here; ++i) {
+    if (i > 0) __syncthreads();  // the next block's prologue refills slots other waves just read
+    process(!a.causal ? item : i == 0 ? heavy : item);
   }
 }
 
 template <typename Tag, int D>
 hipError_t launch_typed(PrefillArgs args, hipStream_t stream) {
   args.q_blocks = (args.seqlen_q + kPpBlockM - 1) / kPpBlockM;
-  const int blocks = args.q_blocks * args.batch * args.heads;
+  const int items_per_bh = args.causal ? (args.q_blocks + 1) / 2 : args.q_blocks;
+  const int blocks = items_per_bh * args.batch * args.heads;
   hipLaunchKernelGGL((prefill_pp_kernel<Tag, D>), dim3(blocks), dim3(kPpThreads), 0, stream, args);
   return hipGetLastError();
 }
