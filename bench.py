@@ -162,13 +162,26 @@ def check_prefill(out, q, k, v, causal, rows) -> dict:
     return {"max_err_vs_fp64": err, "max_err_torch_vs_fp64": err_torch, "correct": ok}
 
 
+WARMUP_MIN_S = 0.1  # warm up for at least this long: the clock settles within tens of ms
+
+
 def time_op(run, steps: int, warmup: int, flush=None) -> tuple[list[float], float]:
     """Per-step event times (ms) on the current stream, the stream the op launches its kernels
-    on, and the wall time of the whole timed region (synchronized on both sides)."""
+    on, and the wall time of the whole timed region (synchronized on both sides). Warmup is at
+    least `warmup` steps and at least WARMUP_MIN_S of work, so the timed steps run at the clock the
+    GPU settles at under this load rather than on its way there after an idle spell (the
+    correctness check before each workload runs on the CPU)."""
     import torch
 
-    for _ in range(warmup):
+    t0 = time.perf_counter()
+    done = 0
+    while done < warmup or (time.perf_counter() - t0 < WARMUP_MIN_S and done < 1000):
+        if flush is not None:
+            flush.zero_()
         run()
+        done += 1
+        if done % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]

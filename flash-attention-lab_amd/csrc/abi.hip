@@ -45,13 +45,14 @@ int elem_bytes(int32_t dtype) { return dtype == FL_DTYPE_F32 ? 4 : 2; }
 bool valid_scale(double s) { return std::isfinite(s) && s > 0.0; }
 
 // Decode workgroups per CU that the split heuristic aims for (FLASH_LAB_DECODE_WG_PER_CU
-// overrides it for experiments).
+// overrides it for experiments). Eight gave the best bandwidth at 32K keys for B=1 MHA and B=8 GQA
+// on MI355X (B=8 MHA is within 2% of its best either way).
 int decode_target_wg_per_cu() {
   if (const char* env = std::getenv("FLASH_LAB_DECODE_WG_PER_CU")) {
     const int v = std::atoi(env);
     if (v >= 1 && v <= 64) return v;
   }
-  return 4;
+  return 8;
 }
 
 // Smallest power of two that gives about decode_target_wg_per_cu() workgroups per CU while each

@@ -2,9 +2,9 @@
 // keys, read in place from a [B, S_max, H_kv, D] cache through strides.
 //
 // Serves the decode_splitkv and decode_inplace ops of the reference (csrc/decode/decode.cu:40-347).
-// The arithmetic follows the reference's definitions (q pre-scaled into the log2 domain,
-// exp2 online softmax, fixed-order log-sum-exp merge of the splits, decode.cu:67-75, 116-133,
-// 204-228); the decomposition is this file's own:
+// The arithmetic follows the reference's definitions (scores in the log2 domain, exp2 online
+// softmax, fixed-order log-sum-exp merge of the splits, decode.cu:67-75, 116-133, 204-228); the
+// decomposition is this file's own:
 //
 //  * A workgroup (4 waves) serves one KV head and all the query heads of its group that it is
 //    given (kHeads of them), over one contiguous key range (its split). Every K and V row it reads
@@ -14,7 +14,9 @@
 //    its group's keys and the output columns of its own piece; no lane ever needs another lane's
 //    V data, and the only cross-lane step in the loop is the dot-product reduction of the group.
 //  * Each lane has kUnroll rows of K and of V in flight per iteration (non-temporal loads: the
-//    cache is read once).
+//    cache is read once). The rows stay packed: q.k goes through v_dot2 (bf16, fp16) and V
+//    elements are unpacked one at a time where they are used, which keeps the kernel at few enough
+//    registers for four workgroups per CU.
 //  * At the end the row groups are merged by a fixed butterfly inside each wave, then the four
 //    waves in order through LDS. With one split the workgroup writes o and lse; otherwise it
 //    writes its unnormalized partial output and (max, sum), and decode_merge_kernel combines the
@@ -28,27 +30,83 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-// Cache rows of K and of V each lane has in flight per iteration.
+// Cache rows of K and of V per lane in each of the two register buffers, for workgroups serving
+// fewer than four query heads (FL_DECODE_UNROLL) and four or more (FL_DECODE_UNROLL_GQA, whose
+// per-head state takes more registers).
 #ifndef FL_DECODE_UNROLL
-#define FL_DECODE_UNROLL 8
+#define FL_DECODE_UNROLL 4
 #endif
-constexpr int kUnroll = FL_DECODE_UNROLL;
+#ifndef FL_DECODE_UNROLL_GQA
+#define FL_DECODE_UNROLL_GQA 4
+#endif
+template <int kHeads>
+constexpr int kUnrollFor = kHeads >= 4 ? FL_DECODE_UNROLL_GQA : FL_DECODE_UNROLL;
 constexpr float kLn2 = 0.693147180559945309f;
 
-// Elements of a 16-byte piece as floats.
+// One lane's 16-byte piece of a cache row, per storage type: the dot product with the lane's piece
+// of q (q kept in its storage form and unscaled; bf16 and fp16 pairs go through v_dot2, which
+// multiplies exactly and accumulates in fp32, so K is never unpacked) and element e of a V piece
+// as a float (unpacked right where it is used, so no unpacked copy of the rows in flight is held).
+// Vector elements are copied to scalars before __builtin_bit_cast: bit-casting the element lvalue
+// q[w] directly made the compiler read element 0 for every w.
 template <typename Tag>
-__device__ __forceinline__ void unpack(const u32x4& w, float (&x)[16 / sizeof(typename Elem<Tag>::storage)]) {
-  if constexpr (sizeof(typename Elem<Tag>::storage) == 4) {
+struct Piece;
+
+template <>
+struct Piece<bf16_tag> {
+  using QPiece = u32x4;
+  static __device__ __forceinline__ QPiece load_q(const void* p) { return load16(p); }
+  static __device__ __forceinline__ float dot(const QPiece& q, const u32x4& k) {
+    float d = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) x[e] = __uint_as_float(w[e]);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      x[2 * e] = Elem<Tag>::to_float(static_cast<uint16_t>(w[e] & 0xffffu));
-      x[2 * e + 1] = Elem<Tag>::to_float(static_cast<uint16_t>(w[e] >> 16));
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t qw = q[w];
+      const uint32_t kw = k[w];
+      d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, qw), __builtin_bit_cast(bf16x2, kw), d,
+                                          false);
     }
+    return d;
   }
-}
+  static __device__ __forceinline__ float elem(const u32x4& v, int e) {
+    const uint32_t w = v[e / 2];
+    return __uint_as_float(e % 2 ? (w & 0xffff0000u) : (w << 16));
+  }
+};
+
+template <>
+struct Piece<f16_tag> {
+  using QPiece = u32x4;
+  static __device__ __forceinline__ QPiece load_q(const void* p) { return load16(p); }
+  static __device__ __forceinline__ float dot(const QPiece& q, const u32x4& k) {
+    float d = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t qw = q[w];
+      const uint32_t kw = k[w];
+      d = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, qw), __builtin_bit_cast(f16x2, kw), d, false);
+    }
+    return d;
+  }
+  static __device__ __forceinline__ float elem(const u32x4& v, int e) {
+    const uint32_t w = v[e / 2];
+    return Elem<f16_tag>::to_float(static_cast<uint16_t>(e % 2 ? (w >> 16) : (w & 0xffffu)));
+  }
+};
+
+template <>
+struct Piece<f32_tag> {
+  using QPiece = f32x4;
+  static __device__ __forceinline__ QPiece load_q(const void* p) {
+    return __builtin_bit_cast(f32x4, load16(p));
+  }
+  static __device__ __forceinline__ float dot(const QPiece& q, const u32x4& k) {
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) d = fmaf(q[e], __uint_as_float(k[e]), d);
+    return d;
+  }
+  static __device__ __forceinline__ float elem(const u32x4& v, int e) { return __uint_as_float(v[e]); }
+};
 
 template <typename Tag, int D, int kHeads>
 __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeArgs a) {
@@ -57,6 +115,7 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeArgs
   constexpr int kLPR = D / kEPL;                           // lanes per cache row
   constexpr int kGPW = 64 / kLPR;                          // row groups per wave
   constexpr int kGroups = kWaves * kGPW;                   // row groups per workgroup
+  constexpr int kUnroll = kUnrollFor<kHeads>;
   constexpr int kKeysPerIter = kGroups * kUnroll;
   static_assert(kLPR >= 1 && kLPR <= 64 && 64 % kLPR == 0, "row pieces must tile a wave");
 
@@ -87,14 +146,14 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeArgs
   const int k_begin = split * per_split;
   const int k_end = min(len, k_begin + per_split);
 
-  float q[kHeads][kEPL];
+  using P = Piece<Tag>;
+  typename P::QPiece q[kHeads];
 #pragma unroll
   for (int g = 0; g < kHeads; ++g) {
     const S* qrow = static_cast<const S*>(a.q) + b * a.q_bs + (h0 + g) * a.q_hs;
-    unpack<Tag>(load16(qrow + piece * kEPL), q[g]);
-#pragma unroll
-    for (int e = 0; e < kEPL; ++e) q[g][e] *= a.scale_log2;
+    q[g] = P::load_q(qrow + piece * kEPL);
   }
+  const float sl2 = a.scale_log2;  // scores are q.k * scale_log2 (log2 domain)
 
   float o[kHeads][kEPL];
   float m[kHeads];  // running max, log2 units (same on every lane of a row group)
@@ -110,39 +169,26 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeArgs
   const S* kbase = static_cast<const S*>(a.k) + b * a.k_bs + hkv * a.k_hs + piece * kEPL;
   const S* vbase = static_cast<const S*>(a.v) + b * a.v_bs + hkv * a.v_hs + piece * kEPL;
 
-  for (int base = k_begin; base < k_end; base += kKeysPerIter) {
-    u32x4 kr[kUnroll];
-    u32x4 vr[kUnroll];
-    bool valid[kUnroll];
+  // Batches of kKeysPerIter keys, double-buffered in registers: the next batch's loads are issued
+  // before the current batch is used, so each wave keeps rows in flight while it computes. Keys past
+  // the split's end are clamped to its last row (always a valid, finite row) and masked out of the
+  // softmax, so every load is issued unconditionally.
+  auto load_batch = [&](int base, u32x4 (&kr)[kUnroll], u32x4 (&vr)[kUnroll]) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int key = base + u * kGroups + group;
-      valid[u] = key < k_end;
-      if (valid[u]) {
-        kr[u] = load16_stream(kbase + static_cast<int64_t>(key) * a.k_ss);
-        vr[u] = load16_stream(vbase + static_cast<int64_t>(key) * a.v_ss);
-      } else {
-        kr[u] = u32x4{0, 0, 0, 0};
-        vr[u] = u32x4{0, 0, 0, 0};
-      }
+      const int key = min(base + u * kGroups + group, k_end - 1);
+      kr[u] = load16_stream(kbase + static_cast<int64_t>(key) * a.k_ss);
+      vr[u] = load16_stream(vbase + static_cast<int64_t>(key) * a.v_ss);
     }
-    float kf[kUnroll][kEPL];
-    float vf[kUnroll][kEPL];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      unpack<Tag>(kr[u], kf[u]);
-      unpack<Tag>(vr[u], vf[u]);
-    }
+  };
+  auto use_batch = [&](int base, const u32x4 (&kr)[kUnroll], const u32x4 (&vr)[kUnroll]) {
 #pragma unroll
     for (int g = 0; g < kHeads; ++g) {
       float s[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        float dot = 0.f;
-#pragma unroll
-        for (int e = 0; e < kEPL; ++e) dot = fmaf(q[g][e], kf[u][e], dot);
-        dot = group_sum<kLPR>(dot);
-        s[u] = valid[u] ? dot : -INFINITY;
+        const float dot = group_sum<kLPR>(P::dot(q[g], kr[u])) * sl2;
+        s[u] = base + u * kGroups + group < k_end ? dot : -INFINITY;
       }
       float mx = s[0];
 #pragma unroll
@@ -159,10 +205,19 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeArgs
         const float p = exp2_fast(s[u] - ref);
         lsum += p;
 #pragma unroll
-        for (int e = 0; e < kEPL; ++e) o[g][e] = fmaf(p, vf[u][e], o[g][e]);
+        for (int e = 0; e < kEPL; ++e) o[g][e] = fmaf(p, P::elem(vr[u], e), o[g][e]);
       }
       l[g] = lsum;
     }
+  };
+  u32x4 ka[kUnroll], va[kUnroll], kb[kUnroll], vb[kUnroll];
+  if (k_begin < k_end) load_batch(k_begin, ka, va);
+  for (int base = k_begin; base < k_end; base += 2 * kKeysPerIter) {
+    if (base + kKeysPerIter < k_end) load_batch(base + kKeysPerIter, kb, vb);
+    use_batch(base, ka, va);
+    if (base + kKeysPerIter >= k_end) break;
+    if (base + 2 * kKeysPerIter < k_end) load_batch(base + 2 * kKeysPerIter, ka, va);
+    use_batch(base + kKeysPerIter, kb, vb);
   }
 
   // Merge the row groups of this wave: butterfly over lanes with the same piece.

@@ -53,7 +53,8 @@ def test_version():
 
 @pytest.mark.parametrize(
     "batch,heads,heads_kv,expected_splits",
-    [(1, 32, 32, 32), (8, 32, 32, 4), (8, 32, 8, 16)],
+    # about 8 workgroups per CU: 32 x 64, 256 x 8, 64 x 32
+    [(1, 32, 32, 64), (8, 32, 32, 8), (8, 32, 8, 32)],
     ids=["B1-MHA", "B8-MHA", "B8-GQA"],
 )
 def test_decode_plan_on_256_cus(batch, heads, heads_kv, expected_splits):
