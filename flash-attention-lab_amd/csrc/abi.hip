@@ -44,23 +44,23 @@ int elem_bytes(int32_t dtype) { return dtype == FL_DTYPE_F32 ? 4 : 2; }
 
 bool valid_scale(double s) { return std::isfinite(s) && s > 0.0; }
 
-// Decode workgroups per CU that the split heuristic aims for (FLASH_LAB_DECODE_WG_PER_CU
-// overrides it for experiments). Eight gave the best bandwidth at 32K keys for B=1 MHA and B=8 GQA
-// on MI355X (B=8 MHA is within 2% of its best either way).
-int decode_target_wg_per_cu() {
-  if (const char* env = std::getenv("FLASH_LAB_DECODE_WG_PER_CU")) {
-    const int v = std::atoi(env);
-    if (v >= 1 && v <= 64) return v;
-  }
-  return 8;
+fl::DType decode_dtype(int32_t dtype) {
+  return dtype == FL_DTYPE_BF16 ? fl::DType::bf16 : dtype == FL_DTYPE_F16 ? fl::DType::f16 : fl::DType::f32;
 }
 
-// Smallest power of two that gives about decode_target_wg_per_cu() workgroups per CU while each
-// split of the longest possible sequence keeps at least 256 keys.
-int choose_num_splits(int64_t workgroups, int max_seqlen, int cu_count) {
-  const int64_t target = static_cast<int64_t>(decode_target_wg_per_cu()) * (cu_count > 0 ? cu_count : 256);
+// Largest power of two (at most 128) whose split workgroups all fit on the GPU at once
+// (resident_per_cu per CU; FLASH_LAB_DECODE_WG_PER_CU overrides it for experiments) while each
+// split of the longest possible sequence keeps at least 256 keys. One wave of workgroups that
+// fills the GPU streams the cache with no tail; measured on MI355X at 32K keys, this beat aiming
+// for two or more workgroups per resident slot.
+int choose_num_splits(int64_t workgroups, int max_seqlen, int cu_count, int resident_per_cu) {
+  if (const char* env = std::getenv("FLASH_LAB_DECODE_WG_PER_CU")) {
+    const int v = std::atoi(env);
+    if (v >= 1 && v <= 64) resident_per_cu = v;
+  }
+  const int64_t capacity = static_cast<int64_t>(resident_per_cu) * (cu_count > 0 ? cu_count : 256);
   int n = 1;
-  while (n < 128 && workgroups * n < target && max_seqlen / (2 * n) >= 256) n *= 2;
+  while (n < 128 && workgroups * 2 * n <= capacity && max_seqlen / (2 * n) >= 256) n *= 2;
   return n;
 }
 
@@ -170,12 +170,14 @@ int fl_decode_plan(const fl_decode_params* p, int32_t requested_splits, int32_t 
   if (num_splits == nullptr || workspace_bytes == nullptr)
     return fail(FL_ERR_INVALID, "null output pointer");
   const int group = p->heads / p->heads_kv;
-  const int head_chunks = group / fl::decode_heads_per_workgroup(group);
-  const int64_t workgroups = static_cast<int64_t>(p->batch) * p->heads_kv * head_chunks;
+  const fl::DecodeLayout layout = fl::decode_layout(decode_dtype(p->dtype), p->head_dim, p->heads_kv, group);
+  const int64_t workgroups = static_cast<int64_t>(p->batch) * (p->heads_kv / layout.kv_span) *
+                             (group / layout.heads_per_wg);
   int n = 1;
   if (allow_splits) {
-    n = requested_splits > 0 ? requested_splits
-                             : choose_num_splits(workgroups, p->max_seqlen, cu_count);
+    n = requested_splits > 0
+            ? requested_splits
+            : choose_num_splits(workgroups, p->max_seqlen, cu_count, layout.resident_per_cu);
   }
   *num_splits = n;
   *workspace_bytes =
@@ -203,7 +205,9 @@ int fl_decode(const fl_decode_params* p, fl_stream_t stream) {
     return fail(FL_ERR_INVALID, "o, lse and seq_lens must be aligned to their element size");
 
   const int group = p->heads / p->heads_kv;
-  const int head_chunks = group / fl::decode_heads_per_workgroup(group);
+  const fl::DType dt = decode_dtype(p->dtype);
+  const fl::DecodeLayout layout = fl::decode_layout(dt, p->head_dim, p->heads_kv, group);
+  const int head_chunks = group / layout.heads_per_wg;
   const int64_t blocks = static_cast<int64_t>(p->batch) * p->heads_kv * head_chunks * p->num_splits;
   if (blocks > (int64_t{1} << 24) || static_cast<int64_t>(p->batch) * p->heads > (int64_t{1} << 24))
     return fail(FL_ERR_INVALID, "batch * heads too large");
@@ -232,6 +236,7 @@ int fl_decode(const fl_decode_params* p, fl_stream_t stream) {
   a.max_seqlen = p->max_seqlen;
   a.num_splits = p->num_splits;
   a.head_chunks = head_chunks;
+  a.kv_span = layout.kv_span;
   a.scale_log2 = static_cast<float>(p->softmax_scale * 1.4426950408889634);
   if (p->num_splits > 1) {
     const size_t need =
@@ -242,9 +247,6 @@ int fl_decode(const fl_decode_params* p, fl_stream_t stream) {
     a.partial_ml =
         p->workspace + static_cast<size_t>(p->batch) * p->heads * p->num_splits * p->head_dim;
   }
-  const fl::DType dt = p->dtype == FL_DTYPE_BF16 ? fl::DType::bf16
-                       : p->dtype == FL_DTYPE_F16 ? fl::DType::f16
-                                                  : fl::DType::f32;
   const hipError_t err = fl::launch_decode(a, dt, p->head_dim, static_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail(FL_ERR_LAUNCH, std::string("decode launch: ") + hipGetErrorString(err));
   return FL_OK;

@@ -20,7 +20,10 @@
 //  * At the end the row groups are merged by a fixed butterfly inside each wave, then the four
 //    waves in order through LDS. With one split the workgroup writes o and lse; otherwise it
 //    writes its unnormalized partial output and (max, sum), and decode_merge_kernel combines the
-//    splits in index order. No atomics: results are bitwise reproducible for a given split count.
+//    splits in a fixed order. No atomics: results are bitwise reproducible for a given split count.
+//    (Merging in the split kernel's last workgroup per head group was measured slower: every
+//    workgroup then has to wait for its partials to reach device scope and for an atomic before it
+//    frees its slot, which costs more than the second launch.)
 #include "gfx950.hpp"
 #include "launch.hpp"
 
@@ -108,34 +111,143 @@ struct Piece<f32_tag> {
   static __device__ __forceinline__ float elem(const u32x4& v, int e) { return __uint_as_float(v[e]); }
 };
 
+// LDS layout of merge_splits: the splits' (max, sum) per head, then per-part partial sums.
+template <int kHeads, int D>
+struct MergeShape {
+  static constexpr int kVecs = kHeads * D / 4;       // 4-column output vectors
+  static constexpr int kParts = kThreads / kVecs;    // threads per output vector
+  static constexpr int kFloats = 2 * kHeads * kMaxSplits + (kParts > 1 ? kThreads * 5 : 0);
+  static_assert(kVecs <= kThreads && kThreads % kVecs == 0, "one thread per vector and part");
+};
+
+// Combines the splits of the kHeads consecutive query heads h0 .. h0 + kHeads - 1 of sequence b:
+// m = max_s m_s, l = sum_s l_s 2^(m_s - m), o = sum_s o_s 2^(m_s - m) / l, lse = m ln 2 + ln l;
+// empty splits (m_s = -inf) contribute nothing. All threads of the workgroup take part. Thread t
+// owns one 4-column output vector (t % kVecs) and the splits p, p + kParts, ... (p = t / kVecs), so
+// its loads are independent and in flight together; the kParts partial sums are then added in part
+// order. Every sum has a fixed order, so the result is the same on every run. The pass is short and
+// latency-bound: the first kFirst partial-output loads of each thread do not depend on the maxima
+// and are issued before the (max, sum) pairs are read, so the two loads overlap.
+// `lds` must hold MergeShape::kFloats floats, 16-byte aligned.
 template <typename Tag, int D, int kHeads>
-__global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeArgs a) {
+__device__ __forceinline__ void merge_splits(const DecodeArgs& a, int b, int h0, float* lds) {
+  using S = typename Elem<Tag>::storage;
+  using Shape = MergeShape<kHeads, D>;
+  constexpr int kVecs = Shape::kVecs;
+  constexpr int kParts = Shape::kParts;
+  constexpr int kVecsPerRow = D / 4;
+  constexpr int kFirst = 8;
+  const int tid = threadIdx.x;
+  const int n = a.num_splits;
+  const int n4 = (n + 3) & ~3;
+  float* ms = lds;                        // [kHeads][kMaxSplits], -inf past n up to n4
+  float* ls = lds + kHeads * kMaxSplits;  // [kHeads][kMaxSplits]
+  const int vec = tid % kVecs;
+  const int part = tid / kVecs;
+  const int g = vec / kVecsPerRow;
+  // Slots of the heads are consecutive: slot(g, s) = (b H + h0) n + g n + s.
+  const int64_t slot0 = (static_cast<int64_t>(b) * a.heads + h0) * n;
+  const f32x4* po =
+      reinterpret_cast<const f32x4*>(a.partial_o + (slot0 + g * n) * D) + vec % kVecsPerRow;
+  f32x4 first[kFirst];
+#pragma unroll
+  for (int j = 0; j < kFirst; ++j) {
+    const int s = part + j * kParts;
+    first[j] = s < n ? po[s * kVecsPerRow] : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int i = tid; i < kHeads * n4; i += kThreads) {
+    const int gi = i / n4;
+    const int s = i - gi * n4;
+    f32x2 ml = {-INFINITY, 0.f};
+    if (s < n) ml = *reinterpret_cast<const f32x2*>(a.partial_ml + 2 * (slot0 + gi * n + s));
+    ms[gi * kMaxSplits + s] = ml[0];
+    ls[gi * kMaxSplits + s] = ml[1];
+  }
+  __syncthreads();
+  float mm = -INFINITY;
+  const f32x4* ms4 = reinterpret_cast<const f32x4*>(ms + g * kMaxSplits);
+  for (int s4 = 0; s4 < n4 / 4; ++s4) {
+    const f32x4 v = ms4[s4];
+    mm = fmaxf(mm, fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+  }
+  f32x4 num = {0.f, 0.f, 0.f, 0.f};
+  float den = 0.f;
+  auto add = [&](int s, const f32x4& o_s) {
+    const float m_s = ms[g * kMaxSplits + s];
+    const float f = m_s == -INFINITY ? 0.f : exp2_fast(m_s - mm);
+    den += ls[g * kMaxSplits + s] * f;
+    num += o_s * f;
+  };
+#pragma unroll
+  for (int j = 0; j < kFirst; ++j) {
+    const int s = part + j * kParts;
+    if (s < n) add(s, first[j]);
+  }
+#pragma unroll 8
+  for (int s = part + kFirst * kParts; s < n; s += kParts) add(s, po[s * kVecsPerRow]);
+  if constexpr (kParts > 1) {
+    f32x4* part_o = reinterpret_cast<f32x4*>(lds + 2 * kHeads * kMaxSplits);  // [kParts][kVecs]
+    float* part_l = reinterpret_cast<float*>(part_o + kThreads);              // [kParts][kVecs]
+    part_o[tid] = num;
+    part_l[tid] = den;
+    __syncthreads();
+    if (part == 0) {
+#pragma unroll
+      for (int p = 1; p < kParts; ++p) {
+        num += part_o[p * kVecs + vec];
+        den += part_l[p * kVecs + vec];
+      }
+    }
+  }
+  if (part == 0) {
+    const int h = h0 + g;
+    const int d0 = (vec % kVecsPerRow) * 4;
+    S* orow = static_cast<S*>(a.o) + b * a.o_bs + h * a.o_hs + d0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) orow[e] = Elem<Tag>::from_float(den > 0.f ? num[e] / den : 0.f);
+    if (d0 == 0) a.lse[b * a.heads + h] = den > 0.f ? mm * kLn2 + logf(den) : -INFINITY;
+  }
+}
+
+// Waves per SIMD the register budget must allow: 5 for one head (96 VGPRs), 3 up to four heads
+// (168), 2 for eight. Without the hint the four-head kernel takes 170 VGPRs, which leaves room for
+// only two waves per SIMD.
+template <int kHeads>
+constexpr int kWavesPerSimd = kHeads == 1 ? 5 : kHeads <= 4 ? 3 : 2;
+
+template <typename Tag, int D, int kHeads, int kSpan>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd<kHeads>)))
+decode_split_kernel(const DecodeArgs a) {
   using S = typename Elem<Tag>::storage;
   constexpr int kEPL = 16 / static_cast<int>(sizeof(S));  // elements per 16-byte piece
   constexpr int kLPR = D / kEPL;                           // lanes per cache row
-  constexpr int kGPW = 64 / kLPR;                          // row groups per wave
+  constexpr int kLPK = kLPR * kSpan;                       // lanes per key (kSpan adjacent heads)
+  constexpr int kGPW = 64 / kLPK;                          // row groups per wave
   constexpr int kGroups = kWaves * kGPW;                   // row groups per workgroup
   constexpr int kUnroll = kUnrollFor<kHeads>;
   constexpr int kKeysPerIter = kGroups * kUnroll;
-  static_assert(kLPR >= 1 && kLPR <= 64 && 64 % kLPR == 0, "row pieces must tile a wave");
+  static_assert(kLPK >= 1 && kLPK <= 64 && 64 % kLPK == 0, "row pieces must tile a wave");
 
-  __shared__ float red_o[kWaves][kHeads][D];
-  __shared__ float red_m[kWaves][kHeads];
-  __shared__ float red_l[kWaves][kHeads];
+  __shared__ float red_o[kWaves][kSpan * kHeads][D];
+  __shared__ float red_m[kWaves][kSpan * kHeads];
+  __shared__ float red_l[kWaves][kSpan * kHeads];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int piece = lane % kLPR;                   // which 16-byte piece of a row
-  const int group = wave * kGPW + lane / kLPR;     // row group within the workgroup
+  const int sp = (lane / kLPR) % kSpan;            // which KV head of the workgroup's span
+  const int group = wave * kGPW + lane / kLPK;     // row group within the workgroup
 
   int w = blockIdx.x;
   const int split = w % a.num_splits;
   w /= a.num_splits;
   const int hchunk = w % a.head_chunks;
   w /= a.head_chunks;
-  const int hkv = w % a.heads_kv;
-  const int b = w / a.heads_kv;
+  const int hblocks = a.heads_kv / kSpan;
+  const int hblk = w % hblocks;
+  const int b = w / hblocks;
+  const int hkv = hblk * kSpan + sp;
   const int h0 = hkv * a.group + hchunk * kHeads;
 
   // Lengths are not checked on the host (that would need a sync); clamp them to the cache so an
@@ -222,7 +334,7 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeArgs
 
   // Merge the row groups of this wave: butterfly over lanes with the same piece.
 #pragma unroll
-  for (int mask = kLPR; mask < 64; mask <<= 1) {
+  for (int mask = kLPK; mask < 64; mask <<= 1) {
 #pragma unroll
     for (int g = 0; g < kHeads; ++g) {
       const float m_o = __shfl_xor(m[g], mask);
@@ -240,22 +352,22 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeArgs
       m[g] = m_new;
     }
   }
-  if (lane < kLPR) {
+  if (lane < kLPK) {  // row group 0 of the wave: one lane per (head of the span, piece)
 #pragma unroll
     for (int g = 0; g < kHeads; ++g) {
 #pragma unroll
-      for (int e = 0; e < kEPL; ++e) red_o[wave][g][piece * kEPL + e] = o[g][e];
-      if (lane == 0) {
-        red_m[wave][g] = m[g];
-        red_l[wave][g] = l[g];
+      for (int e = 0; e < kEPL; ++e) red_o[wave][sp * kHeads + g][piece * kEPL + e] = o[g][e];
+      if (piece == 0) {
+        red_m[wave][sp * kHeads + g] = m[g];
+        red_l[wave][sp * kHeads + g] = l[g];
       }
     }
   }
   __syncthreads();
 
   // Merge the four waves in order and write o/lse (one split) or the partials.
-  for (int idx = tid; idx < kHeads * D; idx += kThreads) {
-    const int g = idx / D;
+  for (int idx = tid; idx < kSpan * kHeads * D; idx += kThreads) {
+    const int g = idx / D;  // (head of the span) * kHeads + query head
     const int d = idx - g * D;
     float mm = -INFINITY;
 #pragma unroll
@@ -271,7 +383,7 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeArgs
         den += red_l[wv][g] * f;
       }
     }
-    const int h = h0 + g;
+    const int h = (hblk * kSpan + g / kHeads) * a.group + hchunk * kHeads + g % kHeads;
     if (a.num_splits == 1) {
       S* orow = static_cast<S*>(a.o) + b * a.o_bs + h * a.o_hs;
       orow[d] = Elem<Tag>::from_float(den > 0.f ? num / den : 0.f);
@@ -285,75 +397,41 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeArgs
       }
     }
   }
-
 }
 
-// Combines the splits of one (sequence, head): m = max_s m_s, l = sum_s l_s 2^(m_s - m),
-// o = sum_s o_s 2^(m_s - m) / l, lse = m ln 2 + ln l; empty splits (m_s = -inf) contribute
-// nothing. One workgroup per (sequence, head): the (m, l) pairs go through LDS, wave w sums the
-// splits w, w + 4, ... (all its loads independent, so they are in flight together), and the four
-// waves' sums are added in wave order, so the result is the same on every run.
-template <typename Tag, int D>
+// Merge pass: one workgroup per head group (kHeads query heads of one KV head).
+template <typename Tag, int D, int kHeads>
 __global__ void __launch_bounds__(kThreads) decode_merge_kernel(const DecodeArgs a) {
-  using S = typename Elem<Tag>::storage;
-  constexpr int kCols = D / 64;  // output columns per lane
-  __shared__ float m_s[kMaxSplits];
-  __shared__ float l_s[kMaxSplits];
-  __shared__ float part_num[kWaves][D];
-  __shared__ float part_den[kWaves];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int bh = blockIdx.x;
-  const int n = a.num_splits;
-  const float* ml = a.partial_ml + static_cast<int64_t>(bh) * n * 2;
-  const float* po = a.partial_o + static_cast<int64_t>(bh) * n * D;
-  for (int s = tid; s < n; s += kThreads) {
-    m_s[s] = ml[2 * s];
-    l_s[s] = ml[2 * s + 1];
-  }
-  __syncthreads();
-  float mm = -INFINITY;
-  for (int s = 0; s < n; ++s) mm = fmaxf(mm, m_s[s]);
-  float num[kCols] = {};
-  float den = 0.f;
-#pragma unroll 4
-  for (int s = wave; s < n; s += kWaves) {
-    const float ms = m_s[s];
-    const float f = ms == -INFINITY ? 0.f : exp2_fast(ms - mm);
-    den += l_s[s] * f;
-#pragma unroll
-    for (int c = 0; c < kCols; ++c) num[c] += po[s * D + c * 64 + lane] * f;
-  }
-#pragma unroll
-  for (int c = 0; c < kCols; ++c) part_num[wave][c * 64 + lane] = num[c];
-  if (lane == 0) part_den[wave] = den;
-  __syncthreads();
-  if (tid < D) {
-    float total = 0.f;
-    float total_den = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      total += part_num[w][tid];
-      total_den += part_den[w];
-    }
-    const int b = bh / a.heads;
-    const int h = bh - b * a.heads;
-    S* orow = static_cast<S*>(a.o) + b * a.o_bs + h * a.o_hs;
-    orow[tid] = Elem<Tag>::from_float(total_den > 0.f ? total / total_den : 0.f);
-    if (tid == 0) a.lse[bh] = total_den > 0.f ? mm * kLn2 + logf(total_den) : -INFINITY;
+  __shared__ __attribute__((aligned(16))) float lds[MergeShape<kHeads, D>::kFloats];
+  int w = blockIdx.x;
+  const int hchunk = w % a.head_chunks;
+  w /= a.head_chunks;
+  const int hkv = w % a.heads_kv;
+  const int b = w / a.heads_kv;
+  merge_splits<Tag, D, kHeads>(a, b, hkv * a.group + hchunk * kHeads, lds);
+}
+
+template <typename Tag, int D, int kHeads, int kSpan>
+void launch_split(const DecodeArgs& args, int groups, hipStream_t stream) {
+  constexpr int kLPR = D * static_cast<int>(sizeof(typename Elem<Tag>::storage)) / 16;
+  if constexpr (kSpan * kLPR <= 64) {
+    hipLaunchKernelGGL((decode_split_kernel<Tag, D, kHeads, kSpan>),
+                       dim3(groups / kSpan * args.num_splits), dim3(kThreads), 0, stream, args);
   }
 }
 
 template <typename Tag, int D, int kHeads>
 hipError_t launch_heads(const DecodeArgs& args, hipStream_t stream) {
-  const int blocks = args.batch * args.heads_kv * args.head_chunks * args.num_splits;
-  hipLaunchKernelGGL((decode_split_kernel<Tag, D, kHeads>), dim3(blocks), dim3(kThreads), 0, stream,
-                     args);
+  const int groups = args.batch * args.heads_kv * args.head_chunks;
+  switch (args.kv_span) {
+    case 4: launch_split<Tag, D, kHeads, 4>(args, groups, stream); break;
+    case 2: launch_split<Tag, D, kHeads, 2>(args, groups, stream); break;
+    default: launch_split<Tag, D, kHeads, 1>(args, groups, stream); break;
+  }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || args.num_splits == 1) return err;
-  hipLaunchKernelGGL((decode_merge_kernel<Tag, D>), dim3(args.batch * args.heads), dim3(kThreads),
-                     0, stream, args);
+  hipLaunchKernelGGL((decode_merge_kernel<Tag, D, kHeads>), dim3(groups), dim3(kThreads), 0, stream,
+                     args);
   return hipGetLastError();
 }
 
@@ -376,10 +454,25 @@ hipError_t launch_type(const DecodeArgs& args, int head_dim, int k_heads, hipStr
 }  // namespace
 }  // namespace decode
 
-int decode_heads_per_workgroup(int group) {
+DecodeLayout decode_layout(DType dtype, int head_dim, int heads_kv, int group) {
+  DecodeLayout layout{};
   int k = 1;
   while (k < 8 && group % (2 * k) == 0) k *= 2;
-  return k;
+  layout.heads_per_wg = k;
+  // Lanes per cache row: 16-byte pieces of head_dim elements. A span of s KV heads puts s * lanes
+  // per row on one key, which must fit a wave.
+  const int lanes_per_row = head_dim * (dtype == DType::f32 ? 4 : 2) / 16;
+  layout.kv_span = 1;
+  for (int s = 4; s > 1; s /= 2) {
+    if (heads_kv % s == 0 && s * lanes_per_row <= 64) {
+      layout.kv_span = s;
+      break;
+    }
+  }
+  layout.resident_per_cu = k == 1 ? decode::kWavesPerSimd<1>
+                           : k <= 4 ? decode::kWavesPerSimd<4>
+                                    : decode::kWavesPerSimd<8>;
+  return layout;
 }
 
 hipError_t launch_decode(const DecodeArgs& args, DType dtype, int head_dim, hipStream_t stream) {

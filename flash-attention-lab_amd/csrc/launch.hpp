@@ -40,7 +40,8 @@ struct DecodeArgs {
   int64_t o_bs, o_hs;
   int batch, heads, heads_kv, group, max_seqlen;
   int num_splits;
-  int head_chunks;   // group / heads served per workgroup
+  int head_chunks;   // group / query heads served per workgroup (of each KV head)
+  int kv_span;       // adjacent KV heads per workgroup (1, 2 or 4; divides heads_kv)
   float scale_log2;  // q is multiplied by this, so scores are in the log2 domain
   float* partial_o;  // [B, H, num_splits, D] unnormalized fp32 partial outputs
   float* partial_ml; // [B, H, num_splits, 2] (max in log2 units, sum) per split
@@ -60,8 +61,15 @@ hipError_t launch_prefill(const PrefillArgs& args, DType dtype, int head_dim, hi
 hipError_t launch_prefill_pingpong(const PrefillArgs& args, DType dtype, int head_dim,
                                    hipStream_t stream);
 
-// Query heads one decode workgroup serves for a GQA group size (a power of two dividing it).
-int decode_heads_per_workgroup(int group);
+// How decode work is laid out: each workgroup serves heads_per_wg query heads (a power of two
+// dividing the GQA group) of each of kv_span adjacent KV heads, and a CU holds resident_per_cu such
+// workgroups at once (their register budget).
+struct DecodeLayout {
+  int heads_per_wg;
+  int kv_span;
+  int resident_per_cu;
+};
+DecodeLayout decode_layout(DType dtype, int head_dim, int heads_kv, int group);
 hipError_t launch_decode(const DecodeArgs& args, DType dtype, int head_dim, hipStream_t stream);
 
 hipError_t launch_axpy(const float* x, const float* y, float alpha, float* out, int64_t n,

@@ -53,8 +53,10 @@ def test_version():
 
 @pytest.mark.parametrize(
     "batch,heads,heads_kv,expected_splits",
-    # about 8 workgroups per CU: 32 x 64, 256 x 8, 64 x 32
-    [(1, 32, 32, 64), (8, 32, 32, 8), (8, 32, 8, 32)],
+    # The largest power of two whose workgroups all fit at once. MHA: 4 KV heads per workgroup,
+    # 5 resident per CU (1280): 8 x 128 and 64 x 16 workgroups. GQA (4 query heads per KV head):
+    # 4 KV heads per workgroup, 3 resident per CU (768): 16 x 32.
+    [(1, 32, 32, 128), (8, 32, 32, 16), (8, 32, 8, 32)],
     ids=["B1-MHA", "B8-MHA", "B8-GQA"],
 )
 def test_decode_plan_on_256_cus(batch, heads, heads_kv, expected_splits):
