@@ -15,6 +15,7 @@
 //  * Work order: the 1-D grid is remapped so each XCD (workgroups are dealt round-robin over the
 //    8 XCDs) runs a contiguous range of (batch, head) pairs and their K/V stay in that XCD's L2.
 //    Within a (batch, head) the causal query blocks run heaviest first.
+#include <cstdlib>
 #include <type_traits>
 
 #include "launch.hpp"
@@ -383,9 +384,25 @@ static_assert(kPrefillBlockN == prefill::kBlockN, "host and kernel tile widths d
 #define FL_PREFILL_PINGPONG 1
 #endif
 
+// Below this many ping-pong workgroups (256 query rows each, causal blocks paired; one per CU) a
+// D = 128 problem runs on this kernel instead, whose 128-row workgroups (two per CU) spread a
+// short prompt over more CUs. Measured on MI355X at B=1, H=32, causal: S=1024 takes 24.6 us here
+// against 42.7 us on the ping-pong kernel (64 workgroups), S=2048 ties, S=4096 (256 ping-pong
+// workgroups) is 128 us there against 161 us here. FLASH_LAB_PREFILL_PP_MIN_WG overrides it (read
+// on every call, so tests can route one shape to either kernel).
+int prefill_pp_min_workgroups() {
+  if (const char* env = std::getenv("FLASH_LAB_PREFILL_PP_MIN_WG")) return std::atoi(env);
+  return 256;
+}
+
 hipError_t launch_prefill(const PrefillArgs& args, DType dtype, int head_dim, hipStream_t stream) {
   using namespace prefill;
-  if (FL_PREFILL_PINGPONG && head_dim == 128) return launch_prefill_pingpong(args, dtype, head_dim, stream);
+  if (FL_PREFILL_PINGPONG && head_dim == 128) {
+    const int64_t pp_blocks = (args.seqlen_q + 255) / 256;
+    const int64_t pp_items = args.causal ? (pp_blocks + 1) / 2 : pp_blocks;
+    if (pp_items * args.batch * args.heads >= prefill_pp_min_workgroups())
+      return launch_prefill_pingpong(args, dtype, head_dim, stream);
+  }
   if (dtype == DType::bf16) {
     return head_dim == 64 ? launch_typed<bf16_tag, 64>(args, stream)
                           : launch_typed<bf16_tag, 128>(args, stream);

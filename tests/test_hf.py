@@ -41,8 +41,12 @@ def test_register_with_transformers():
     import flash_lab.hf
 
     name = flash_lab.hf.register()
-    assert name == "flash_lab"
-    assert name in transformers.AttentionInterface._global_mapping
+    mapping = transformers.AttentionInterface._global_mapping
+    assert "flash_lab" in mapping and name in mapping
+    # transformers 5 reads any name containing "flash" as a flash-attention kernel to import, so
+    # the function is reachable under "fl_lab" there; older versions take "flash_lab" itself.
+    assert name == ("fl_lab" if flash_lab.hf.reserved_by_transformers("flash_lab") else "flash_lab")
+    assert not flash_lab.hf.reserved_by_transformers(name)
 
 
 @pytest.mark.gpu
@@ -87,3 +91,16 @@ def test_decode_step_uses_position_ids_as_lengths(decode_impl):
         )
         assert out.shape == (3, 1, 8, 128)
         torch.testing.assert_close(out.cpu().double(), ref, atol=2e-2, rtol=0)
+
+
+def test_sequence_ends_are_read_once_per_position_tensor():
+    from flash_lab import hf
+
+    positions = torch.arange(10).expand(2, 10).clone()
+    assert hf._sequence_ends(positions) == {9}
+    cached = hf._last_ends
+    assert hf._sequence_ends(positions) == {9} and hf._last_ends is cached  # no second read
+    positions[1, -1] = 12  # an in-place change is seen through the version counter
+    assert hf._sequence_ends(positions) == {9, 12}
+    other = torch.arange(5).expand(1, 5)  # another tensor is read afresh
+    assert hf._sequence_ends(other) == {4}
