@@ -5,7 +5,8 @@
 Metric: prefill TFLOP/s at (B, H, H_kv, S, D) = (4, 32, 32, 4096, 128) bf16 and
 split-KV decode GB/s at 32K keys. A step is one prefill forward over that batch (non-causal), the
 configuration the metric is quoted on; `value` is its throughput. The causal prefill and the three
-decode configurations (B=1 MHA, B=8 MHA, B=8 GQA, 32K keys) are reported under "secondary".
+decode configurations (B=1 MHA, B=8 MHA, B=8 GQA, 32K keys; B=8 GQA also as a paged cache of
+16-row blocks) are reported under "secondary".
 
 Inputs are synthetic iid N(0, 1) bf16 from torch.Generator(device="cuda").manual_seed(0), drawn in
 the reference's order (q, k, v; decode q, k_cache, v_cache: reference bench/run.py:122-141), and
@@ -47,6 +48,8 @@ DECODE = {
     "B1-MHA": dict(batch=1, heads=32, heads_kv=32, context=32768, head_dim=128),
     "B8-MHA": dict(batch=8, heads=32, heads_kv=32, context=32768, head_dim=128),
     "B8-GQA": dict(batch=8, heads=32, heads_kv=8, context=32768, head_dim=128),
+    # The same cache in 16-row blocks of a pool, in shuffled order (block_tables).
+    "B8-GQA-paged16": dict(batch=8, heads=32, heads_kv=8, context=32768, head_dim=128, page_size=16),
 }
 
 
@@ -244,7 +247,23 @@ def bench_decode(name: str, steps: int, warmup: int, flush) -> dict:
     k_cache = torch.randn((b, ctx, hkv, d), generator=gen, device="cuda", dtype=torch.bfloat16)
     v_cache = torch.randn((b, ctx, hkv, d), generator=gen, device="cuda", dtype=torch.bfloat16)
     seq_lens = torch.full((b,), ctx, dtype=torch.int32, device="cuda")
-    out = flash_lab.decode(q, k_cache, v_cache, seq_lens)
+    tables = None
+    page_size = cfg.get("page_size")
+    if page_size:
+        # Scatter the cache into shuffled blocks of a pool; the check below reads the contiguous
+        # copy, which holds the same rows.
+        per_seq = ctx // page_size
+        order = torch.randperm(b * per_seq, generator=gen, device="cuda")
+        tables = order.view(b, per_seq).to(torch.int32)
+        pools = []
+        for cache in (k_cache, v_cache):
+            pool = torch.empty((b * per_seq, page_size, hkv, d), device="cuda", dtype=torch.bfloat16)
+            pool[order] = cache.reshape(b * per_seq, page_size, hkv, d)
+            pools.append(pool)
+        k_used, v_used = pools
+    else:
+        k_used, v_used = k_cache, v_cache
+    out = flash_lab.decode(q, k_used, v_used, seq_lens, block_tables=tables)
     # Check the first sequence in full against fp64 (the reference checks all of them; one keeps
     # the CPU side short at 32K keys), with the reference's rule.
     args = (q[:1].cpu(), k_cache[:1].cpu(), v_cache[:1].cpu(), seq_lens[:1].cpu())
@@ -255,16 +274,19 @@ def bench_decode(name: str, steps: int, warmup: int, flush) -> dict:
     ok = bool(torch.isfinite(out).all()) and err <= 2 * err_torch + 1e-3
     if not ok:
         return {"status": "incorrect", "max_err_vs_fp64": err, "max_err_torch_vs_fp64": err_torch}
-    times, _ = time_op(lambda: flash_lab.decode(q, k_cache, v_cache, seq_lens), steps, warmup, flush)
+    del k_cache, v_cache
+    times, _ = time_op(lambda: flash_lab.decode(q, k_used, v_used, seq_lens, block_tables=tables),
+                       steps, warmup, flush)
     stats = summarize(times)
     mean_ms = sum(times) / len(times)
     kv = decode_kv_bytes(b, hkv, ctx, d, 2)
     splits, _ = _hip.decode_plan(b, h, hkv, d, ctx, torch.bfloat16,
                                  cu_count_=_hip.cu_count(torch.cuda.current_device()))
-    del q, k_cache, v_cache
+    del q, k_used, v_used, tables
     torch.cuda.empty_cache()
     return {
         "status": "ok",
+        "page_size": page_size,
         "kv_bytes": kv,
         "bytes_with_q_o": decode_bytes_with_qo(b, h, hkv, ctx, d, 2),
         "num_splits": splits,

@@ -53,6 +53,13 @@ fl::DType decode_dtype(int32_t dtype) {
 // split of the longest possible sequence keeps at least 256 keys. One wave of workgroups that
 // fills the GPU streams the cache with no tail; measured on MI355X at 32K keys, this beat aiming
 // for two or more workgroups per resident slot.
+// Cache blocks one split may touch at most: its keys (rounded up to the kernel's largest batch of
+// 128 keys) over page_size, plus a partial block at each end.
+int64_t pages_per_split(int max_seqlen, int num_splits, int page_size) {
+  const int64_t keys = (static_cast<int64_t>(max_seqlen) + num_splits - 1) / num_splits + 127;
+  return keys / page_size + 2;
+}
+
 int choose_num_splits(int64_t workgroups, int max_seqlen, int cu_count, int resident_per_cu) {
   if (const char* env = std::getenv("FLASH_LAB_DECODE_WG_PER_CU")) {
     const int v = std::atoi(env);
@@ -66,6 +73,8 @@ int choose_num_splits(int64_t workgroups, int max_seqlen, int cu_count, int resi
 
 int check_decode_shape(const fl_decode_params* p) {
   if (p == nullptr) return fail(FL_ERR_INVALID, "null decode parameters");
+  if (p->block_tables != nullptr && (p->page_size <= 0 || p->num_blocks <= 0))
+    return fail(FL_ERR_INVALID, "a paged cache needs page_size > 0 and num_blocks > 0");
   if (p->dtype != FL_DTYPE_BF16 && p->dtype != FL_DTYPE_F16 && p->dtype != FL_DTYPE_F32)
     return fail(FL_ERR_UNSUPPORTED, "decode takes bf16, fp16, or fp32");
   if (p->head_dim != 64 && p->head_dim != 128)
@@ -179,6 +188,14 @@ int fl_decode_plan(const fl_decode_params* p, int32_t requested_splits, int32_t 
             ? requested_splits
             : choose_num_splits(workgroups, p->max_seqlen, cu_count, layout.resident_per_cu);
   }
+  if (p->block_tables != nullptr && allow_splits && requested_splits == 0) {
+    // A paged split stages its block numbers in LDS: take more splits if one would touch too many.
+    while (n < fl::kMaxSplits && pages_per_split(p->max_seqlen, n, p->page_size) > fl::kMaxSplitPages)
+      n *= 2;
+  }
+  if (p->block_tables != nullptr && pages_per_split(p->max_seqlen, n, p->page_size) > fl::kMaxSplitPages)
+    return fail(FL_ERR_UNSUPPORTED,
+                "paged cache too long for the split count (at most 1024 blocks per split)");
   *num_splits = n;
   *workspace_bytes =
       n > 1 ? static_cast<size_t>(p->batch) * p->heads * n * (p->head_dim + 2) * sizeof(float) : 0;
@@ -195,14 +212,23 @@ int fl_decode(const fl_decode_params* p, fl_stream_t stream) {
   const int eb = elem_bytes(p->dtype);
   if (!rows_16_byte(p->q, eb, p->batch, p->q_batch_stride, p->heads, p->q_head_stride, 1, 0))
     return fail(FL_ERR_INVALID, "q must have 16-byte aligned rows");
-  if (!rows_16_byte(p->k_cache, eb, p->batch, p->k_batch_stride, p->max_seqlen, p->k_seq_stride,
-                    p->heads_kv, p->k_head_stride))
+  // Cache dimensions: [B, S_max] rows, or [num_blocks, page_size] for a paged cache.
+  const int64_t outer = p->block_tables != nullptr ? p->num_blocks : p->batch;
+  const int64_t rows = p->block_tables != nullptr ? p->page_size : p->max_seqlen;
+  if (!rows_16_byte(p->k_cache, eb, outer, p->k_batch_stride, rows, p->k_seq_stride, p->heads_kv,
+                    p->k_head_stride))
     return fail(FL_ERR_INVALID, "k_cache must have 16-byte aligned rows (data pointer and strides)");
-  if (!rows_16_byte(p->v_cache, eb, p->batch, p->v_batch_stride, p->max_seqlen, p->v_seq_stride,
-                    p->heads_kv, p->v_head_stride))
+  if (!rows_16_byte(p->v_cache, eb, outer, p->v_batch_stride, rows, p->v_seq_stride, p->heads_kv,
+                    p->v_head_stride))
     return fail(FL_ERR_INVALID, "v_cache must have 16-byte aligned rows (data pointer and strides)");
   if (!aligned(p->o, eb) || !aligned(p->lse, 4) || !aligned(p->seq_lens, 4))
     return fail(FL_ERR_INVALID, "o, lse and seq_lens must be aligned to their element size");
+  if (p->block_tables != nullptr) {
+    if (!aligned(p->block_tables, 4)) return fail(FL_ERR_INVALID, "block_tables must be 4-byte aligned");
+    if (pages_per_split(p->max_seqlen, p->num_splits, p->page_size) > fl::kMaxSplitPages)
+      return fail(FL_ERR_UNSUPPORTED,
+                  "paged cache too long for the split count (at most 1024 blocks per split)");
+  }
 
   const int group = p->heads / p->heads_kv;
   const fl::DType dt = decode_dtype(p->dtype);
@@ -237,12 +263,20 @@ int fl_decode(const fl_decode_params* p, fl_stream_t stream) {
   a.num_splits = p->num_splits;
   a.head_chunks = head_chunks;
   a.kv_span = layout.kv_span;
+  a.block_tables = p->block_tables;
+  a.block_tables_stride = p->block_tables_stride;
+  a.page_size = p->page_size;
+  a.num_blocks = p->num_blocks;
+  a.page_shift = -1;
+  for (int s = 0; s < 31; ++s)
+    if (p->page_size == (1 << s)) a.page_shift = s;
   a.scale_log2 = static_cast<float>(p->softmax_scale * 1.4426950408889634);
   if (p->num_splits > 1) {
     const size_t need =
         static_cast<size_t>(p->batch) * p->heads * p->num_splits * (p->head_dim + 2) * sizeof(float);
-    if (p->workspace == nullptr || p->workspace_bytes < need || !aligned(p->workspace, 4))
+    if (p->workspace == nullptr || p->workspace_bytes < need)
       return fail(FL_ERR_INVALID, "decode workspace is missing or smaller than fl_decode_plan reports");
+    if (!aligned(p->workspace, 16)) return fail(FL_ERR_INVALID, "decode workspace must be 16-byte aligned");
     a.partial_o = p->workspace;
     a.partial_ml =
         p->workspace + static_cast<size_t>(p->batch) * p->heads * p->num_splits * p->head_dim;

@@ -215,7 +215,7 @@ __device__ __forceinline__ void merge_splits(const DecodeArgs& a, int b, int h0,
 template <int kHeads>
 constexpr int kWavesPerSimd = kHeads == 1 ? 5 : kHeads <= 4 ? 3 : 2;
 
-template <typename Tag, int D, int kHeads, int kSpan>
+template <typename Tag, int D, int kHeads, int kSpan, bool kPaged>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd<kHeads>)))
 decode_split_kernel(const DecodeArgs a) {
   using S = typename Elem<Tag>::storage;
@@ -278,8 +278,47 @@ decode_split_kernel(const DecodeArgs a) {
     for (int e = 0; e < kEPL; ++e) o[g][e] = 0.f;
   }
 
-  const S* kbase = static_cast<const S*>(a.k) + b * a.k_bs + hkv * a.k_hs + piece * kEPL;
-  const S* vbase = static_cast<const S*>(a.v) + b * a.v_bs + hkv * a.v_hs + piece * kEPL;
+  // Contiguous cache: rows of sequence b at b * bs + key * ss. Paged cache
+  // ([num_blocks, page_size, H_kv, D]): key lives in block block_tables[b][key / page_size], row
+  // key % page_size. The split's block numbers are staged in LDS once (clamped to the cache, so a
+  // bad table entry cannot read outside it); LDS reads do not wait behind the rows in flight.
+  __shared__ int page_table[kPaged ? kMaxSplitPages : 1];
+  int page0 = 0;
+  if constexpr (kPaged) {
+    if (k_begin < k_end) {
+      page0 = k_begin / a.page_size;
+      const int pages = (k_end - 1) / a.page_size - page0 + 1;
+      const int32_t* row = a.block_tables + static_cast<int64_t>(b) * a.block_tables_stride + page0;
+      for (int i = tid; i < pages; i += kThreads) page_table[i] = min(max(row[i], 0), a.num_blocks - 1);
+    }
+    __syncthreads();
+  }
+  const S* kbase = static_cast<const S*>(a.k) + (kPaged ? 0 : b * a.k_bs) + hkv * a.k_hs + piece * kEPL;
+  const S* vbase = static_cast<const S*>(a.v) + (kPaged ? 0 : b * a.v_bs) + hkv * a.v_hs + piece * kEPL;
+  // (block, row) of a key; page sizes that are powers of two (the usual ones) take a shift.
+  auto locate = [&](int key, int& block, int& row) {
+    const int page = a.page_shift >= 0 ? key >> a.page_shift : key / a.page_size;
+    block = page_table[page - page0];
+    row = key - page * a.page_size;
+  };
+  auto k_row = [&](int key) -> const S* {
+    if constexpr (kPaged) {
+      int block, row;
+      locate(key, block, row);
+      return kbase + static_cast<int64_t>(block) * a.k_bs + static_cast<int64_t>(row) * a.k_ss;
+    } else {
+      return kbase + static_cast<int64_t>(key) * a.k_ss;
+    }
+  };
+  auto v_row = [&](int key) -> const S* {
+    if constexpr (kPaged) {
+      int block, row;
+      locate(key, block, row);
+      return vbase + static_cast<int64_t>(block) * a.v_bs + static_cast<int64_t>(row) * a.v_ss;
+    } else {
+      return vbase + static_cast<int64_t>(key) * a.v_ss;
+    }
+  };
 
   // Batches of kKeysPerIter keys, double-buffered in registers: the next batch's loads are issued
   // before the current batch is used, so each wave keeps rows in flight while it computes. Keys past
@@ -289,8 +328,8 @@ decode_split_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int key = min(base + u * kGroups + group, k_end - 1);
-      kr[u] = load16_stream(kbase + static_cast<int64_t>(key) * a.k_ss);
-      vr[u] = load16_stream(vbase + static_cast<int64_t>(key) * a.v_ss);
+      kr[u] = load16_stream(k_row(key));
+      vr[u] = load16_stream(v_row(key));
     }
   };
   auto use_batch = [&](int base, const u32x4 (&kr)[kUnroll], const u32x4 (&vr)[kUnroll]) {
@@ -415,8 +454,14 @@ template <typename Tag, int D, int kHeads, int kSpan>
 void launch_split(const DecodeArgs& args, int groups, hipStream_t stream) {
   constexpr int kLPR = D * static_cast<int>(sizeof(typename Elem<Tag>::storage)) / 16;
   if constexpr (kSpan * kLPR <= 64) {
-    hipLaunchKernelGGL((decode_split_kernel<Tag, D, kHeads, kSpan>),
-                       dim3(groups / kSpan * args.num_splits), dim3(kThreads), 0, stream, args);
+    const dim3 grid(groups / kSpan * args.num_splits);
+    if (args.block_tables != nullptr) {
+      hipLaunchKernelGGL((decode_split_kernel<Tag, D, kHeads, kSpan, true>), grid, dim3(kThreads), 0,
+                         stream, args);
+    } else {
+      hipLaunchKernelGGL((decode_split_kernel<Tag, D, kHeads, kSpan, false>), grid, dim3(kThreads),
+                         0, stream, args);
+    }
   }
 }
 

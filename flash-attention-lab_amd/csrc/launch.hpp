@@ -45,10 +45,18 @@ struct DecodeArgs {
   float scale_log2;  // q is multiplied by this, so scores are in the log2 domain
   float* partial_o;  // [B, H, num_splits, D] unnormalized fp32 partial outputs
   float* partial_ml; // [B, H, num_splits, 2] (max in log2 units, sum) per split
+  // Paged cache (block_tables non-null): k/v are [num_blocks, page_size, H_kv, D], k_bs/v_bs the
+  // block strides, block_tables [B, *] int32 with row stride block_tables_stride.
+  const int32_t* block_tables;
+  int64_t block_tables_stride;
+  int page_size, num_blocks;
+  int page_shift;  // log2(page_size) when it is a power of two, else -1
 };
 
 // Largest split count a decode call may use.
 constexpr int kMaxSplits = 128;
+// Most cache blocks one split of a paged decode may touch (its block numbers are staged in LDS).
+constexpr int kMaxSplitPages = 1024;
 
 enum class DType : int { bf16 = 0, f16 = 1, f32 = 2 };
 

@@ -91,6 +91,10 @@ class DecodeParams(ctypes.Structure):
         ("softmax_scale", ctypes.c_double),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
+        ("block_tables", ctypes.c_void_p),
+        ("block_tables_stride", ctypes.c_int64),
+        ("page_size", ctypes.c_int32),
+        ("num_blocks", ctypes.c_int32),
     ]
 
 
@@ -256,8 +260,18 @@ def prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, sof
 # Decode
 
 
-def _decode_params(q, k_cache, v_cache, seq_lens, o, lse, softmax_scale) -> DecodeParams:
+def _decode_params(q, k_cache, v_cache, seq_lens, o, lse, softmax_scale,
+                   block_tables=None) -> DecodeParams:
     batch, heads, head_dim = q.shape
+    if block_tables is not None:
+        # [num_blocks, page_size, H_kv, D] caches: the batch strides are block strides.
+        p = _decode_params(q, k_cache, v_cache, seq_lens, o, lse, softmax_scale)
+        p.max_seqlen = block_tables.shape[1] * k_cache.shape[1]
+        p.block_tables = block_tables.data_ptr()
+        p.block_tables_stride = block_tables.stride(0)
+        p.page_size = k_cache.shape[1]
+        p.num_blocks = k_cache.shape[0]
+        return p
     return DecodeParams(
         q.data_ptr(),
         k_cache.data_ptr(),
@@ -284,9 +298,12 @@ def _decode_params(q, k_cache, v_cache, seq_lens, o, lse, softmax_scale) -> Deco
     )
 
 
-def decode(q, k_cache, v_cache, seq_lens, softmax_scale: float, num_splits: int, allow_splits: bool):
+def decode(q, k_cache, v_cache, seq_lens, softmax_scale: float, num_splits: int, allow_splits: bool,
+           block_tables=None):
     """Op-boundary checks of the reference (csrc/decode/decode_host.h:18-53,
-    csrc/decode/decode.cu:286-311), output and workspace allocation, fl_decode_plan + fl_decode."""
+    csrc/decode/decode.cu:286-311), output and workspace allocation, fl_decode_plan + fl_decode.
+    With block_tables the caches are paged, [num_blocks, page_size, H_kv, D] (a layout the
+    reference defines but none of its kernels runs)."""
     _check_cuda(q=q, k_cache=k_cache, v_cache=v_cache, seq_lens=seq_lens)
     _require(q.dtype in DTYPE_CODES, "decode takes bf16, fp16, or fp32")
     _require(
@@ -296,10 +313,24 @@ def decode(q, k_cache, v_cache, seq_lens, softmax_scale: float, num_splits: int,
     _require(seq_lens.dtype == torch.int32, "seq_lens must have dtype int32")
     _require(q.dim() == 3 and k_cache.dim() == 4, "q must be [B, H, D], caches [B, S_max, H_kv, D]")
     _require(k_cache.shape == v_cache.shape, "k_cache and v_cache must have the same shape")
-    _require(
-        k_cache.shape[0] == q.shape[0] and k_cache.shape[3] == q.shape[2],
-        "q and the caches must agree on batch size and head_dim",
-    )
+    if block_tables is None:
+        _require(
+            k_cache.shape[0] == q.shape[0] and k_cache.shape[3] == q.shape[2],
+            "q and the caches must agree on batch size and head_dim",
+        )
+    else:
+        _check_cuda(block_tables=block_tables)
+        _require(block_tables.dtype == torch.int32, "block_tables must have dtype int32")
+        _require(
+            block_tables.dim() == 2 and block_tables.shape[0] == q.shape[0]
+            and block_tables.shape[1] >= 1 and block_tables.stride(1) == 1,
+            "block_tables must be [B, max_blocks] with unit stride in its last dimension",
+        )
+        _require(k_cache.shape[3] == q.shape[2], "q and the caches must agree on head_dim")
+        _require(
+            block_tables.shape[1] * k_cache.shape[1] < 2**31,
+            "paged cache too long (max_blocks * page_size must fit in int32)",
+        )
     _require(seq_lens.dim() == 1 and seq_lens.shape[0] == q.shape[0], "seq_lens must be [B]")
     _require(seq_lens.is_contiguous(), "seq_lens must be contiguous")
     for name, x in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
@@ -308,7 +339,7 @@ def decode(q, k_cache, v_cache, seq_lens, softmax_scale: float, num_splits: int,
 
     o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty(q.shape[:2], dtype=torch.float32, device=q.device)
-    p = _decode_params(q, k_cache, v_cache, seq_lens, o, lse, softmax_scale)
+    p = _decode_params(q, k_cache, v_cache, seq_lens, o, lse, softmax_scale, block_tables)
     splits = ctypes.c_int32()
     ws_bytes = ctypes.c_size_t()
     index = q.device.index if q.device.index is not None else torch.cuda.current_device()
@@ -356,6 +387,12 @@ DECODE_SCHEMA = (
     "(Tensor q, Tensor k_cache, Tensor v_cache, Tensor seq_lens, float softmax_scale,"
     " int num_splits) -> (Tensor, Tensor)"
 )
+# Paged-cache decode has no op in the reference (its kernels reject paged caches): the same
+# schema with the block tables after seq_lens.
+PAGED_DECODE_SCHEMA = (
+    "(Tensor q, Tensor k_cache, Tensor v_cache, Tensor seq_lens, Tensor block_tables,"
+    " float softmax_scale, int num_splits) -> (Tensor, Tensor)"
+)
 
 
 def _register() -> None:
@@ -390,8 +427,28 @@ def _register() -> None:
 
     prefill_op("attention_mma_pipelined")
     prefill_op("attention_mma")
+    def paged_decode_op(name, allow_splits):
+        @torch.library.custom_op(
+            f"{lib}::{name}", mutates_args=(), device_types="cuda", schema=PAGED_DECODE_SCHEMA
+        )
+        def op(
+            q: torch.Tensor,
+            k_cache: torch.Tensor,
+            v_cache: torch.Tensor,
+            seq_lens: torch.Tensor,
+            block_tables: torch.Tensor,
+            softmax_scale: float,
+            num_splits: int,
+        ) -> tuple[torch.Tensor, torch.Tensor]:
+            return decode(q, k_cache, v_cache, seq_lens, softmax_scale, num_splits, allow_splits,
+                          block_tables)
+
+        return op
+
     decode_op("decode_splitkv", True)
     decode_op("decode_inplace", False)
+    paged_decode_op("decode_splitkv_paged", True)
+    paged_decode_op("decode_inplace_paged", False)
 
     @torch.library.custom_op(
         f"{lib}::smoke_axpy", mutates_args=(), device_types="cuda",
@@ -451,6 +508,8 @@ OPS = (
     "attention_mma",
     "decode_splitkv",
     "decode_inplace",
+    "decode_splitkv_paged",
+    "decode_inplace_paged",
     "smoke_axpy",
     "mma_tile_test",
 )

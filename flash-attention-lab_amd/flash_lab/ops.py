@@ -56,8 +56,12 @@ class DecodeImpl:
     op: str
     dtypes: tuple[torch.dtype, ...]
     head_dims: tuple[int, ...]
-    paged: bool = False
+    paged_op: str | None = None  # the op serving paged caches (None: paged caches unsupported)
     in_auto: bool = True  # False for baselines kept for comparison only
+
+    @property
+    def paged(self) -> bool:
+        return self.paged_op is not None
 
     def unsupported_reason(self, shape: DecodeShape, dtype: torch.dtype) -> str | None:
         if dtype not in self.dtypes:
@@ -85,8 +89,12 @@ PREFILL_IMPLS: dict[str, PrefillImpl] = {
 }
 _DECODE_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 DECODE_IMPLS: dict[str, DecodeImpl] = {
-    "splitkv": DecodeImpl(op="decode_splitkv", dtypes=_DECODE_DTYPES, head_dims=_DIMS),
-    "decode_inplace": DecodeImpl(op="decode_inplace", dtypes=_DECODE_DTYPES, head_dims=_DIMS),
+    "splitkv": DecodeImpl(
+        op="decode_splitkv", dtypes=_DECODE_DTYPES, head_dims=_DIMS, paged_op="decode_splitkv_paged"
+    ),
+    "decode_inplace": DecodeImpl(
+        op="decode_inplace", dtypes=_DECODE_DTYPES, head_dims=_DIMS, paged_op="decode_inplace_paged"
+    ),
     # The reference's copy-based baseline; not shipped by this build.
     "decode_copy": DecodeImpl(
         op="decode_copy", dtypes=_DECODE_DTYPES, head_dims=_DIMS, in_auto=False
@@ -109,12 +117,17 @@ def _register_fakes() -> None:
     def decode_fake(q, k_cache, v_cache, seq_lens, softmax_scale, num_splits):
         return q.new_empty(q.shape), q.new_empty(q.shape[:2], dtype=torch.float32)
 
+    def paged_decode_fake(q, k_cache, v_cache, seq_lens, block_tables, softmax_scale, num_splits):
+        return q.new_empty(q.shape), q.new_empty(q.shape[:2], dtype=torch.float32)
+
     for spec in PREFILL_IMPLS.values():
         if _op_exists(spec.op):
             torch.library.register_fake(f"flash_lab::{spec.op}")(prefill_fake)
     for spec in DECODE_IMPLS.values():
         if _op_exists(spec.op):
             torch.library.register_fake(f"flash_lab::{spec.op}")(decode_fake)
+        if spec.paged_op and _op_exists(spec.paged_op):
+            torch.library.register_fake(f"flash_lab::{spec.paged_op}")(paged_decode_fake)
 
 
 if HAS_EXTENSION:
@@ -122,9 +135,10 @@ if HAS_EXTENSION:
 
 # All ops are registered by the import above, so availability is looked up once.
 _BUILT_OPS = frozenset(
-    spec.op
+    op
     for spec in (*PREFILL_IMPLS.values(), *DECODE_IMPLS.values())
-    if HAS_EXTENSION and _op_exists(spec.op)
+    for op in (spec.op, getattr(spec, "paged_op", None))
+    if op and HAS_EXTENSION and _op_exists(op)
 )
 
 
@@ -223,9 +237,14 @@ def decode(
         ),
         lambda s: s.unsupported_reason(shape, q.dtype),
     )
-    out, lse = getattr(torch.ops.flash_lab, spec.op)(
-        q3, k_cache, v_cache, seq_lens, scale, num_splits or 0
-    )
+    if block_tables is not None:
+        out, lse = getattr(torch.ops.flash_lab, spec.paged_op)(
+            q3, k_cache, v_cache, seq_lens, block_tables, scale, num_splits or 0
+        )
+    else:
+        out, lse = getattr(torch.ops.flash_lab, spec.op)(
+            q3, k_cache, v_cache, seq_lens, scale, num_splits or 0
+        )
     if q.dim() == 4:
         out = out.unsqueeze(1)
     return (out, lse) if return_lse else out

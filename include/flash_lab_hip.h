@@ -75,8 +75,19 @@ int fl_attention_fwd(const fl_attn_params* p, fl_stream_t stream);
  * [B, H, D]; caches are [B, S_max, H_kv, D] read in place through strides;
  * seq_lens [B] int32 on the device (never read by the host); o [B, H, D] in
  * the input dtype; lse [B, H] fp32 contiguous. num_splits must be resolved
- * by fl_decode_plan first. workspace is fp32 device memory of at least the
- * size fl_decode_plan reports (unused, may be NULL, when num_splits == 1).
+ * by fl_decode_plan first. workspace is 16-byte aligned fp32 device memory of
+ * at least the size fl_decode_plan reports (unused, may be NULL, when
+ * num_splits == 1).
+ *
+ * Paged caches (block_tables != NULL; the reference defines the layout,
+ * flash_lab/layouts.py:145-158, and its oracle, reference.py:155-164, but
+ * every reference kernel rejects it, ops.py:61-62): k_cache and v_cache are
+ * [num_blocks, page_size, H_kv, D] and the *_batch_stride fields are the
+ * block strides; block_tables is [B, max_blocks] int32 on the device with
+ * row stride block_tables_stride, and max_seqlen = max_blocks * page_size.
+ * Key j of sequence b is row j % page_size of block
+ * block_tables[b][j / page_size]; entries outside [0, num_blocks) are
+ * clamped on the device rather than read out of bounds.
  */
 typedef struct fl_decode_params {
   const void* q;
@@ -95,6 +106,9 @@ typedef struct fl_decode_params {
   double softmax_scale;
   float* workspace;
   size_t workspace_bytes;
+  const int32_t* block_tables; /* NULL: contiguous [B, S_max, H_kv, D] caches */
+  int64_t block_tables_stride;
+  int32_t page_size, num_blocks;
 } fl_decode_params;
 
 /*

@@ -40,9 +40,10 @@ def test_library_exports_every_declared_function():
 
 def test_struct_layouts_match_the_header():
     # Natural C alignment: 5 pointers + 12 int64 + 8 int32 + double = 176 bytes;
-    # 6 pointers + 10 int64 + 7 int32 (+4 pad) + double + pointer + size_t = 184 bytes.
+    # 6 pointers + 10 int64 + 7 int32 (+4 pad) + double + pointer + size_t
+    # + pointer + int64 + 2 int32 (paged cache) = 208 bytes.
     assert ctypes.sizeof(_hip.AttnParams) == 176
-    assert ctypes.sizeof(_hip.DecodeParams) == 184
+    assert ctypes.sizeof(_hip.DecodeParams) == 208
     assert _hip.AttnParams.softmax_scale.offset == 168
     assert _hip.DecodeParams.softmax_scale.offset == 160
 
@@ -134,6 +135,57 @@ def test_decode_rejects_missing_workspace():
     p.num_splits = 0
     assert _hip.LIB.fl_decode(ctypes.byref(p), None) != 0
     assert "num_splits must be in [1, 128]" in _hip.LIB.fl_last_error().decode()
+
+
+def _paged_params(page_size, max_blocks, num_blocks=64):
+    p = _hip.DecodeParams()
+    p.q = p.k_cache = p.v_cache = p.o = p.lse = p.seq_lens = p.workspace = 256
+    p.batch, p.heads, p.heads_kv, p.head_dim = 1, 8, 8, 128
+    p.max_seqlen = max_blocks * page_size
+    p.q_batch_stride, p.q_head_stride = 8 * 128, 128
+    p.k_batch_stride = p.v_batch_stride = page_size * 8 * 128
+    p.k_seq_stride = p.v_seq_stride = 8 * 128
+    p.k_head_stride = p.v_head_stride = 128
+    p.o_batch_stride, p.o_head_stride = 8 * 128, 128
+    p.dtype, p.softmax_scale = 0, 0.1
+    p.block_tables, p.block_tables_stride = 256, max_blocks
+    p.page_size, p.num_blocks = page_size, num_blocks
+    return p
+
+
+def test_paged_plan_bounds_the_blocks_per_split():
+    # A paged split stages its block numbers in LDS (at most 1024): the plan takes more splits
+    # when one would touch more blocks, and refuses a requested count that is too small.
+    splits, ws = ctypes.c_int32(), ctypes.c_size_t()
+    p = _paged_params(page_size=1, max_blocks=100000)
+    p.batch = 64  # the occupancy rule alone would pick 8 splits: 12,629 blocks each
+    assert _hip.LIB.fl_decode_plan(ctypes.byref(p), 0, 1, 256, ctypes.byref(splits),
+                                   ctypes.byref(ws)) == 0
+    assert splits.value == 128  # 782 keys, at most 911 blocks per split
+    assert _hip.LIB.fl_decode_plan(ctypes.byref(p), 4, 1, 256, ctypes.byref(splits),
+                                   ctypes.byref(ws)) != 0
+    assert "1024 blocks" in _hip.LIB.fl_last_error().decode()
+    p = _paged_params(page_size=1, max_blocks=200000)  # too long even at 128 splits
+    assert _hip.LIB.fl_decode_plan(ctypes.byref(p), 0, 1, 256, ctypes.byref(splits),
+                                   ctypes.byref(ws)) != 0
+    p = _paged_params(page_size=16, max_blocks=64)
+    assert _hip.LIB.fl_decode_plan(ctypes.byref(p), 0, 0, 256, ctypes.byref(splits),
+                                   ctypes.byref(ws)) == 0
+    assert splits.value == 1  # decode_inplace
+
+
+def test_paged_decode_rejects_bad_geometry():
+    p = _paged_params(page_size=0, max_blocks=4)
+    assert _hip.LIB.fl_decode(ctypes.byref(p), None) != 0
+    assert "page_size" in _hip.LIB.fl_last_error().decode()
+    p = _paged_params(page_size=16, max_blocks=4, num_blocks=0)
+    assert _hip.LIB.fl_decode(ctypes.byref(p), None) != 0
+    assert "num_blocks" in _hip.LIB.fl_last_error().decode()
+    p = _paged_params(page_size=16, max_blocks=4)
+    p.block_tables = 258  # not 4-byte aligned
+    p.num_splits = 1
+    assert _hip.LIB.fl_decode(ctypes.byref(p), None) != 0
+    assert "block_tables" in _hip.LIB.fl_last_error().decode()
 
 
 def test_tile_test_rejects_bad_k():

@@ -107,10 +107,6 @@ def test_rejects_unsupported(impl):
     seq_lens = torch.tensor([8], device="cuda", dtype=torch.int32)
     with pytest.raises(ValueError, match="head_dim"):
         flash_lab.decode(q, cache, cache, seq_lens, impl=impl)
-    q, cache = q[..., :64], torch.randn(4, 4, 4, 64, device="cuda", dtype=torch.bfloat16)
-    tables = torch.zeros(1, 2, device="cuda", dtype=torch.int32)
-    with pytest.raises(ValueError, match="paged"):
-        flash_lab.decode(q.contiguous(), cache, cache, seq_lens, block_tables=tables, impl=impl)
 
 
 @pytest.mark.parametrize(
@@ -158,3 +154,110 @@ def test_lengths_outside_the_cache_are_clamped():
     empty = torch.tensor([0, 100], device="cuda", dtype=torch.int32)
     out, lse = flash_lab.decode(q, k_cache, v_cache, empty, return_lse=True)
     assert torch.all(out[0] == 0) and torch.isneginf(lse[0]).all()
+
+
+# Paged caches: [num_blocks, page_size, H_kv, D] pools with per-sequence block tables. The
+# reference defines the layout and its oracle (flash_lab/layouts.py:145-158, reference.py:155-164)
+# but every reference kernel rejects it; here both decode impls run it.
+
+
+def to_paged(cache, page_size, gen, spare=5):
+    """Scatters a contiguous [B, S_max, H_kv, D] cache into shuffled blocks of a larger pool."""
+    batch, max_seqlen = cache.shape[:2]
+    per_seq = -(-max_seqlen // page_size)
+    padded = torch.zeros(batch, per_seq * page_size, *cache.shape[2:], dtype=cache.dtype,
+                         device=cache.device)
+    padded[:, :max_seqlen] = cache
+    num_blocks = batch * per_seq + spare
+    order = torch.randperm(num_blocks, generator=gen)[: batch * per_seq].to(cache.device)
+    pool = torch.randn(num_blocks, page_size, *cache.shape[2:], dtype=cache.dtype,
+                       device=cache.device)  # unused blocks hold noise
+    pool[order] = padded.reshape(batch * per_seq, page_size, *cache.shape[2:])
+    return pool, order.view(batch, per_seq).to(torch.int32)
+
+
+PAGED_CASES = [
+    # batch, heads, heads_kv, max_seqlen, head_dim, seq_lens, page_size
+    (3, 8, 2, 300, 128, [300, 1, 157], 16),
+    (2, 32, 8, 2000, 128, [2000, 1333], 64),
+    (4, 8, 8, 129, 64, [129, 64, 65, 3], 1),
+    (2, 6, 2, 500, 64, [500, 250], 7),  # a page size that is not a power of two
+    (1, 32, 32, 4096, 128, [4096], 256),
+]
+
+
+@pytest.mark.parametrize("case", PAGED_CASES, ids=lambda c: f"B{c[0]}-H{c[1]}-Hkv{c[2]}-S{c[3]}-D{c[4]}-P{c[6]}")
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).removeprefix("torch."))
+@pytest.mark.parametrize("impl", IMPLS)
+def test_paged_matches_reference(impl, dtype, case):
+    print(f"paged decode {impl} {dtype} {case}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    *contig, page_size = case
+    q, k_cache, v_cache, seq_lens = make_case(tuple(contig), dtype, gen)
+    cpu_gen = torch.Generator().manual_seed(4)
+    k_pool, tables = to_paged(k_cache, page_size, cpu_gen)
+    cpu_gen = torch.Generator().manual_seed(4)
+    v_pool, _ = to_paged(v_cache, page_size, cpu_gen)
+    out, lse = flash_lab.decode(q, k_pool, v_pool, seq_lens, block_tables=tables, impl=impl,
+                                return_lse=True)
+    # The oracle reads the pool through the same tables (reference.py:155-164).
+    ref, ref_lse = reference.decode(q.cpu(), k_pool.cpu(), v_pool.cpu(), seq_lens.cpu(),
+                                    block_tables=tables.cpu(), return_lse=True)
+    plain_ref = reference.decode(q.cpu(), k_cache.cpu(), v_cache.cpu(), seq_lens.cpu())
+    torch.testing.assert_close(ref, plain_ref, rtol=0, atol=0)  # the pool holds the same rows
+    check_decode(out, lse, q, k_cache, v_cache, seq_lens)
+
+
+@pytest.mark.parametrize("num_splits", [1, 4, 32])
+def test_paged_equals_contiguous_bitwise(num_splits):
+    # Same keys in the same order per split: a paged cache must give the contiguous cache's bits.
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    q, k_cache, v_cache, seq_lens = make_case((3, 32, 8, 3000, 128, [3000, 17, 2048]),
+                                              torch.bfloat16, gen)
+    cpu_gen = torch.Generator().manual_seed(9)
+    k_pool, tables = to_paged(k_cache, 32, cpu_gen)
+    cpu_gen = torch.Generator().manual_seed(9)
+    v_pool, _ = to_paged(v_cache, 32, cpu_gen)
+    want = flash_lab.decode(q, k_cache, v_cache, seq_lens, num_splits=num_splits, return_lse=True)
+    got = flash_lab.decode(q, k_pool, v_pool, seq_lens, block_tables=tables,
+                           num_splits=num_splits, return_lse=True)
+    assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+
+
+def test_paged_block_numbers_outside_the_pool_are_clamped():
+    # Table entries are device data the host never reads; out-of-range ones are clamped to the
+    # pool instead of read out of bounds.
+    gen = torch.Generator(device="cuda").manual_seed(10)
+    q, k_cache, v_cache, seq_lens = make_case((2, 4, 4, 64, 64, [64, 40]), torch.float32, gen)
+    pool = torch.randn(6, 16, 4, 64, device="cuda", generator=gen)
+    bad = torch.tensor([[0, 99, -5, 2], [5, 1000000, 3, 4]], device="cuda", dtype=torch.int32)
+    clamped = bad.clamp(0, 5)
+    out = flash_lab.decode(q, pool, pool, seq_lens, block_tables=bad)
+    want = flash_lab.decode(q, pool, pool, seq_lens, block_tables=clamped)
+    assert torch.isfinite(out).all() and torch.equal(out, want)
+
+
+def test_paged_decode_in_a_graph():
+    # The paged step captures in a HIP graph like the contiguous one (no host reads).
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    q, k_cache, v_cache, seq_lens = make_case((2, 16, 4, 1024, 128, [1024, 500]), torch.bfloat16, gen)
+    cpu_gen = torch.Generator().manual_seed(12)
+    k_pool, tables = to_paged(k_cache, 16, cpu_gen)
+    cpu_gen = torch.Generator().manual_seed(12)
+    v_pool, _ = to_paged(v_cache, 16, cpu_gen)
+    eager = flash_lab.decode(q, k_pool, v_pool, seq_lens, block_tables=tables)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        flash_lab.decode(q, k_pool, v_pool, seq_lens, block_tables=tables)  # warm up off-graph
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = flash_lab.decode(q, k_pool, v_pool, seq_lens, block_tables=tables)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager)
+        eager_again = flash_lab.decode(q, k_pool, v_pool, seq_lens, block_tables=tables)
+        torch.cuda.synchronize()
+        assert torch.equal(eager_again, eager)

@@ -42,6 +42,23 @@ def test_decode_compiles_without_graph_breaks(impl):
     )
 
 
+def test_paged_decode_compiles_without_graph_breaks():
+    torch._dynamo.reset()
+
+    def step(q, k_pool, v_pool, seq_lens, tables):
+        return flash_lab.decode(q, k_pool, v_pool, seq_lens, block_tables=tables) * 2
+
+    q = torch.randn(2, 1, 8, 128, device="cuda", dtype=torch.bfloat16)
+    k_pool = torch.randn(40, 16, 2, 128, device="cuda", dtype=torch.bfloat16)
+    v_pool = torch.randn(40, 16, 2, 128, device="cuda", dtype=torch.bfloat16)
+    tables = torch.randperm(40, device="cuda")[:32].view(2, 16).to(torch.int32)
+    seq_lens = torch.tensor([256, 77], device="cuda", dtype=torch.int32)
+    compiled = torch.compile(step, fullgraph=True)
+    torch.testing.assert_close(
+        compiled(q, k_pool, v_pool, seq_lens, tables), step(q, k_pool, v_pool, seq_lens, tables)
+    )
+
+
 def test_decode_replays_in_a_hip_graph():
     # generate() captures the decode step; the op allocates its outputs and workspace from the
     # caching allocator and launches on the current stream, so it can be captured. Each replay is
