@@ -167,16 +167,10 @@ def check_prefill(out, q, k, v, causal, rows) -> dict:
 
 WARMUP_MIN_S = 0.1  # warm up for at least this long: the clock settles within tens of ms
 
-# GPU clock / power / temperature sampler (flash_lab.observe), open while main() runs, and what it
-# saw during the last timed region.
-CLOCKS = None
-LAST_CLOCKS = None
-
 
 def time_op(run, steps: int, warmup: int, flush=None) -> tuple[list[float], float]:
     """Per-step event times (ms) on the current stream, the stream the op launches its kernels
-    on, and the wall time of the whole timed region (synchronized on both sides); the GPU clocks
-    sampled during that region go to LAST_CLOCKS. Warmup is at
+    on, and the wall time of the whole timed region (synchronized on both sides). Warmup is at
     least `warmup` steps and at least WARMUP_MIN_S of work, so the timed steps run at the clock the
     GPU settles at under this load rather than on its way there after an idle spell (the
     correctness check before each workload runs on the CPU)."""
@@ -195,7 +189,6 @@ def time_op(run, steps: int, warmup: int, flush=None) -> tuple[list[float], floa
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     torch.cuda.synchronize()
-    stamp = time.time()
     t0 = time.perf_counter()
     for i in range(steps):
         if flush is not None:
@@ -205,8 +198,6 @@ def time_op(run, steps: int, warmup: int, flush=None) -> tuple[list[float], floa
         ends[i].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    global LAST_CLOCKS
-    LAST_CLOCKS = CLOCKS.window(stamp, time.time()) if CLOCKS is not None else None
     return [s.elapsed_time(e) for s, e in zip(starts, ends)], wall
 
 
@@ -222,7 +213,6 @@ def bench_prefill(steps: int, warmup: int, causal: bool) -> dict:
     if not check["correct"]:
         return {"status": "incorrect", **check}
     times, wall = time_op(lambda: flash_lab.attention(q, k, v, causal=causal), steps, warmup)
-    gpu = LAST_CLOCKS
     flops = attention_flops(cfg["batch"], cfg["heads"], cfg["seqlen"], cfg["seqlen"],
                             cfg["head_dim"], causal)
     mean_ms = sum(times) / len(times)
@@ -239,7 +229,6 @@ def bench_prefill(steps: int, warmup: int, causal: bool) -> dict:
         "tflops": flops / (stats["median"] / 1e3) / 1e12,
         "tflops_mean": flops / (mean_ms / 1e3) / 1e12,
         "frac_of_peak": flops / (mean_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS,
-        "gpu_during_timing": gpu,
         **check,
     }
 
@@ -288,7 +277,6 @@ def bench_decode(name: str, steps: int, warmup: int, flush) -> dict:
     del k_cache, v_cache
     times, _ = time_op(lambda: flash_lab.decode(q, k_used, v_used, seq_lens, block_tables=tables),
                        steps, warmup, flush)
-    gpu = LAST_CLOCKS
     stats = summarize(times)
     mean_ms = sum(times) / len(times)
     kv = decode_kv_bytes(b, hkv, ctx, d, 2)
@@ -313,7 +301,6 @@ def bench_decode(name: str, steps: int, warmup: int, flush) -> dict:
                                    "for the split and merge kernels"},
         "max_err_vs_fp64": err,
         "max_err_torch_vs_fp64": err_torch,
-        "gpu_during_timing": gpu,
     }
 
 
@@ -427,12 +414,8 @@ def main(argv=None) -> int:
         print(f"the HIP library did not load: {ops.EXTENSION_ERROR}", file=sys.stderr)
         return 2
 
-    from flash_lab.observe import ClockSampler
-
-    global CLOCKS
     props = torch.cuda.get_device_properties(0)
     workloads = selected_workloads(args.only)
-    CLOCKS = ClockSampler(interval_ms=20).__enter__()
     secondary = {}
     headline = None
     if "prefill" in workloads:
@@ -493,13 +476,11 @@ def main(argv=None) -> int:
             "softmax_scale": 1 / math.sqrt(PREFILL["head_dim"]),
         },
         "roofline": roofline,
-        "gpu_during_timing": headline.get("gpu_during_timing") if headline else None,
         "cpu_baseline": None,
         "secondary": secondary,
         "device": {"name": props.name, "cus": props.multi_processor_count,
                    "arch": getattr(props, "gcnArchName", "")},
     }
-    CLOCKS.__exit__(None, None, None)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

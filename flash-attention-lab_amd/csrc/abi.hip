@@ -50,9 +50,10 @@ fl::DType decode_dtype(int32_t dtype) {
 
 // Largest power of two (at most 128) whose split workgroups all fit on the GPU at once
 // (resident_per_cu per CU; FLASH_LAB_DECODE_WG_PER_CU overrides it for experiments) while each
-// split of the longest possible sequence keeps at least 256 keys. One wave of workgroups that
+// split of the longest possible sequence keeps at least 512 keys. One wave of workgroups that
 // fills the GPU streams the cache with no tail; measured on MI355X at 32K keys, this beat aiming
-// for two or more workgroups per resident slot.
+// for two or more workgroups per resident slot, and splits of 256 keys (B=1 MHA, 128 splits)
+// lost about 1% to 512-key ones (64 splits).
 // Cache blocks one split may touch at most: its keys (rounded up to the kernel's largest batch of
 // 128 keys) over page_size, plus a partial block at each end.
 int64_t pages_per_split(int max_seqlen, int num_splits, int page_size) {
@@ -67,7 +68,7 @@ int choose_num_splits(int64_t workgroups, int max_seqlen, int cu_count, int resi
   }
   const int64_t capacity = static_cast<int64_t>(resident_per_cu) * (cu_count > 0 ? cu_count : 256);
   int n = 1;
-  while (n < 128 && workgroups * 2 * n <= capacity && max_seqlen / (2 * n) >= 256) n *= 2;
+  while (n < 128 && workgroups * 2 * n <= capacity && max_seqlen / (2 * n) >= 512) n *= 2;
   return n;
 }
 

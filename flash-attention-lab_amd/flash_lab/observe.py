@@ -4,7 +4,8 @@ The counterparts of the reference's bench/clocks.py (an nvidia-smi sampler) and 
 ranges of bench/decode_trace.py, for MI355X:
 
 * ClockSampler samples the shader (gfx) and memory clocks, socket power and hotspot temperature
-  of one GPU through the amdsmi Python bindings in a background thread, with host timestamps;
+  of one GPU through the amdsmi Python bindings, in a background thread or on demand (sample()),
+  with host timestamps;
   window(start, end) reports min / median / max over a time window (one benchmark). On gfx950 the
   shader clock under sustained MFMA load settles well below its 2.4 GHz maximum (power limit), so
   a throughput figure is only interpretable next to the clock it ran at.
@@ -101,6 +102,9 @@ class ClockSampler:
         if sample is None:
             return self
         self.available = True
+        self._sample = sample
+        if self.interval_s <= 0:  # no background thread: the caller samples with sample()
+            return self
 
         def loop():
             while not self._stop.is_set():
@@ -111,6 +115,13 @@ class ClockSampler:
         self._thread = threading.Thread(target=loop, daemon=True)
         self._thread.start()
         return self
+
+    def sample(self) -> None:
+        """Takes one sample now, in the calling thread. A background thread in a Python process
+        that is busy launching kernels holds the interpreter lock rarely, so for short regions
+        the caller samples explicitly while it waits for the GPU (bench.py does)."""
+        if self.available:
+            self.samples.append((time.time(), self._sample()))
 
     def __exit__(self, *exc) -> None:
         self._stop.set()

@@ -54,10 +54,11 @@ def test_version():
 
 @pytest.mark.parametrize(
     "batch,heads,heads_kv,expected_splits",
-    # The largest power of two whose workgroups all fit at once. MHA: 4 KV heads per workgroup,
-    # 5 resident per CU (1280): 8 x 128 and 64 x 16 workgroups. GQA (4 query heads per KV head):
-    # 4 KV heads per workgroup, 3 resident per CU (768): 16 x 32.
-    [(1, 32, 32, 128), (8, 32, 32, 16), (8, 32, 8, 32)],
+    # The largest power of two whose workgroups all fit at once, with >= 512 keys per split. MHA:
+    # 4 KV heads per workgroup, 5 resident per CU (1280): 8 x 64 (the 512-key floor) and 64 x 16
+    # workgroups. GQA (4 query heads per KV head): 4 KV heads per workgroup, 3 resident per CU
+    # (768): 16 x 32.
+    [(1, 32, 32, 64), (8, 32, 32, 16), (8, 32, 8, 32)],
     ids=["B1-MHA", "B8-MHA", "B8-GQA"],
 )
 def test_decode_plan_on_256_cus(batch, heads, heads_kv, expected_splits):
@@ -73,9 +74,9 @@ def test_decode_plan_requested_and_inplace():
         1,
         0,
     )
-    # Short caches keep >= 256 keys per split.
-    assert _hip.decode_plan(1, 8, 8, 128, 500, torch.bfloat16)[0] == 1
-    assert _hip.decode_plan(1, 8, 8, 128, 512, torch.bfloat16)[0] == 2
+    # Short caches keep >= 512 keys per split.
+    assert _hip.decode_plan(1, 8, 8, 128, 1000, torch.bfloat16)[0] == 1
+    assert _hip.decode_plan(1, 8, 8, 128, 1024, torch.bfloat16)[0] == 2
 
 
 def test_decode_plan_rejections():
