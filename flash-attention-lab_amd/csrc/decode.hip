@@ -1,22 +1,25 @@
 // Split-KV decode for gfx950: one query token per sequence against its first seq_lens[b] cached
-// keys, read in place from a [B, S_max, H_kv, D] cache through strides.
+// keys, read in place through strides from a [B, S_max, H_kv, D] cache or a paged
+// [num_blocks, page_size, H_kv, D] pool with per-sequence block tables.
 //
-// Serves the decode_splitkv and decode_inplace ops of the reference (csrc/decode/decode.cu:40-347).
-// The arithmetic follows the reference's definitions (scores in the log2 domain, exp2 online
+// Serves the decode_splitkv and decode_inplace ops of the reference (csrc/decode/decode.cu:40-347)
+// and their paged forms (a layout the reference defines, flash_lab/layouts.py:145-158, but does not
+// run). The arithmetic follows the reference's definitions (scores in the log2 domain, exp2 online
 // softmax, fixed-order log-sum-exp merge of the splits, decode.cu:67-75, 116-133, 204-228); the
 // decomposition is this file's own:
 //
-//  * A workgroup (4 waves) serves one KV head and all the query heads of its group that it is
-//    given (kHeads of them), over one contiguous key range (its split). Every K and V row it reads
-//    serves all kHeads heads.
+//  * A workgroup (4 waves) serves kSpan adjacent KV heads (4 where they divide H_kv, so one key's
+//    rows of the span are one contiguous 1 KiB segment at D = 128 bf16) and, for each, the kHeads
+//    query heads of its group it is given, over one contiguous key range (its split). Every K and
+//    V row it reads serves all kHeads heads of its KV head.
 //  * A cache row (D elements) is read as 16-byte pieces by a group of D * elem / 16 lanes, so
 //    every load instruction moves whole rows. Each lane keeps, per head, the running max and sum of
 //    its group's keys and the output columns of its own piece; no lane ever needs another lane's
 //    V data, and the only cross-lane step in the loop is the dot-product reduction of the group.
-//  * Each lane has kUnroll rows of K and of V in flight per iteration (non-temporal loads: the
-//    cache is read once). The rows stay packed: q.k goes through v_dot2 (bf16, fp16) and V
-//    elements are unpacked one at a time where they are used, which keeps the kernel at few enough
-//    registers for four workgroups per CU.
+//  * Each lane has kUnroll rows of K and of V in flight in each of two register buffers
+//    (non-temporal loads: the cache is read once). The rows stay packed: q.k goes through v_dot2
+//    (bf16, fp16) and V elements are unpacked one at a time where they are used, which keeps the
+//    kernel at 96 registers for one query head (five workgroups per CU) and 168 up to four.
 //  * At the end the row groups are merged by a fixed butterfly inside each wave, then the four
 //    waves in order through LDS. With one split the workgroup writes o and lse; otherwise it
 //    writes its unnormalized partial output and (max, sum), and decode_merge_kernel combines the
