@@ -168,7 +168,14 @@ def check_prefill(out, q, k, v, causal, rows) -> dict:
 WARMUP_MIN_S = 0.1  # warm up for at least this long: the clock settles within tens of ms
 
 
-def time_op(run, steps: int, warmup: int, flush=None) -> tuple[list[float], float]:
+# --trace: every timed step runs inside a roctx range "<workload>:step" that ends after a device
+# synchronize (the reference's bench/decode_trace.py:1-8 with NVTX), so `rocprofv3 --marker-trace
+# --kernel-trace` attributes each kernel to its step. The synchronize changes the timing, so a
+# traced run is for attribution, not for the JSON figures.
+TRACE = False
+
+
+def time_op(run, steps: int, warmup: int, flush=None, label: str = "step") -> tuple[list[float], float]:
     """Per-step event times (ms) on the current stream, the stream the op launches its kernels
     on, and the wall time of the whole timed region (synchronized on both sides). Warmup is at
     least `warmup` steps and at least WARMUP_MIN_S of work, so the timed steps run at the clock the
@@ -193,6 +200,15 @@ def time_op(run, steps: int, warmup: int, flush=None) -> tuple[list[float], floa
     for i in range(steps):
         if flush is not None:
             flush.zero_()
+        if TRACE:
+            from flash_lab.observe import roctx_range
+
+            with roctx_range(f"{label}:step"):
+                starts[i].record()
+                run()
+                ends[i].record()
+                torch.cuda.synchronize()
+            continue
         starts[i].record()
         run()
         ends[i].record()
@@ -212,7 +228,8 @@ def bench_prefill(steps: int, warmup: int, causal: bool) -> dict:
     check = check_prefill(flash_lab.attention(q, k, v, causal=causal), q, k, v, causal, rows)
     if not check["correct"]:
         return {"status": "incorrect", **check}
-    times, wall = time_op(lambda: flash_lab.attention(q, k, v, causal=causal), steps, warmup)
+    times, wall = time_op(lambda: flash_lab.attention(q, k, v, causal=causal), steps, warmup,
+                          label="prefill_causal" if causal else "prefill")
     flops = attention_flops(cfg["batch"], cfg["heads"], cfg["seqlen"], cfg["seqlen"],
                             cfg["head_dim"], causal)
     mean_ms = sum(times) / len(times)
@@ -276,7 +293,7 @@ def bench_decode(name: str, steps: int, warmup: int, flush) -> dict:
         return {"status": "incorrect", "max_err_vs_fp64": err, "max_err_torch_vs_fp64": err_torch}
     del k_cache, v_cache
     times, _ = time_op(lambda: flash_lab.decode(q, k_used, v_used, seq_lens, block_tables=tables),
-                       steps, warmup, flush)
+                       steps, warmup, flush, label=name)
     stats = summarize(times)
     mean_ms = sum(times) / len(times)
     kv = decode_kv_bytes(b, hkv, ctx, d, 2)
@@ -355,6 +372,9 @@ def parse_args(argv=None):
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--decode-steps", type=int, default=100)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--trace", action="store_true",
+                        help="roctx range per timed step, for rocprofv3 --marker-trace (timings "
+                             "then include a synchronize per step)")
     parser.add_argument(
         "--only",
         help="comma list of workloads to run: prefill, prefill_causal, decode (all three), "
@@ -414,6 +434,8 @@ def main(argv=None) -> int:
         print(f"the HIP library did not load: {ops.EXTENSION_ERROR}", file=sys.stderr)
         return 2
 
+    global TRACE
+    TRACE = args.trace
     props = torch.cuda.get_device_properties(0)
     workloads = selected_workloads(args.only)
     secondary = {}

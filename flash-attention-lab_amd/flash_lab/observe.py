@@ -9,7 +9,7 @@ ranges of bench/decode_trace.py, for MI355X:
   window(start, end) reports min / median / max over a time window (one benchmark). On gfx950 the
   shader clock under sustained MFMA load settles well below its 2.4 GHz maximum (power limit), so
   a throughput figure is only interpretable next to the clock it ran at.
-* roctx_range(name) pushes and pops a roctx range (libroctx64), which `rocprofv3 --marker-trace`
+* roctx_range(name) pushes and pops a roctx range (rocprofiler-sdk roctx), which `rocprofv3 --marker-trace`
   records, so every kernel of a benchmark step can be attributed to that step.
 
 Both degrade to no-ops where the library or the GPU is missing (the CPU test machine), and neither
@@ -159,7 +159,10 @@ def _roctx():
     global _ROCTX, _ROCTX_TRIED
     if not _ROCTX_TRIED:
         _ROCTX_TRIED = True
-        for name in ("libroctx64.so", "/opt/rocm/lib/libroctx64.so"):
+        # rocprofv3 intercepts the rocprofiler-sdk roctx library; the legacy libroctx64 is the
+        # fallback for older tools.
+        for name in ("librocprofiler-sdk-roctx.so", "/opt/rocm/lib/librocprofiler-sdk-roctx.so",
+                     "libroctx64.so", "/opt/rocm/lib/libroctx64.so"):
             try:
                 lib = ctypes.CDLL(name)
             except OSError:
@@ -175,7 +178,7 @@ def _roctx():
 
 @contextlib.contextmanager
 def roctx_range(name: str):
-    """A roctx range around the block (no-op without libroctx64)."""
+    """A roctx range around the block (no-op without a roctx library)."""
     lib = _roctx()
     if lib is not None:
         lib.roctxRangePushA(name.encode())

@@ -55,3 +55,9 @@ def test_profiled_traffic_is_parsed(tmp_path):
 def test_more_than_one_gpu_is_refused(capsys):
     assert bench.main(["--gpus", "2"]) == 2
     assert "one GPU" in capsys.readouterr().err
+
+
+def test_trace_option_parses():
+    args = bench.parse_args(["--trace", "--only", "decode"])
+    assert args.trace and args.only == "decode"
+    assert not bench.parse_args([]).trace
