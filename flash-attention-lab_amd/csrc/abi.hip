@@ -190,13 +190,11 @@ int fl_decode_plan(const fl_decode_params* p, int32_t requested_splits, int32_t 
             : choose_num_splits(workgroups, p->max_seqlen, cu_count, layout.resident_per_cu);
   }
   if (p->block_tables != nullptr && allow_splits && requested_splits == 0) {
-    // A paged split stages its block numbers in LDS: take more splits if one would touch too many.
+    // A paged split stages its block numbers in LDS when they fit: take more splits if one would
+    // touch too many (a longer split still works, reading the table from global memory).
     while (n < fl::kMaxSplits && pages_per_split(p->max_seqlen, n, p->page_size) > fl::kMaxSplitPages)
       n *= 2;
   }
-  if (p->block_tables != nullptr && pages_per_split(p->max_seqlen, n, p->page_size) > fl::kMaxSplitPages)
-    return fail(FL_ERR_UNSUPPORTED,
-                "paged cache too long for the split count (at most 1024 blocks per split)");
   *num_splits = n;
   *workspace_bytes =
       n > 1 ? static_cast<size_t>(p->batch) * p->heads * n * (p->head_dim + 2) * sizeof(float) : 0;
@@ -224,12 +222,8 @@ int fl_decode(const fl_decode_params* p, fl_stream_t stream) {
     return fail(FL_ERR_INVALID, "v_cache must have 16-byte aligned rows (data pointer and strides)");
   if (!aligned(p->o, eb) || !aligned(p->lse, 4) || !aligned(p->seq_lens, 4))
     return fail(FL_ERR_INVALID, "o, lse and seq_lens must be aligned to their element size");
-  if (p->block_tables != nullptr) {
-    if (!aligned(p->block_tables, 4)) return fail(FL_ERR_INVALID, "block_tables must be 4-byte aligned");
-    if (pages_per_split(p->max_seqlen, p->num_splits, p->page_size) > fl::kMaxSplitPages)
-      return fail(FL_ERR_UNSUPPORTED,
-                  "paged cache too long for the split count (at most 1024 blocks per split)");
-  }
+  if (p->block_tables != nullptr && !aligned(p->block_tables, 4))
+    return fail(FL_ERR_INVALID, "block_tables must be 4-byte aligned");
 
   const int group = p->heads / p->heads_kv;
   const fl::DType dt = decode_dtype(p->dtype);
@@ -268,6 +262,10 @@ int fl_decode(const fl_decode_params* p, fl_stream_t stream) {
   a.block_tables_stride = p->block_tables_stride;
   a.page_size = p->page_size;
   a.num_blocks = p->num_blocks;
+  a.page_table_global =
+      p->block_tables != nullptr &&
+      pages_per_split(p->max_seqlen, p->num_splits, p->page_size) > fl::kMaxSplitPages;
+  if (a.page_table_global) a.kv_span = 1;
   a.page_shift = -1;
   for (int s = 0; s < 31; ++s)
     if (p->page_size == (1 << s)) a.page_shift = s;

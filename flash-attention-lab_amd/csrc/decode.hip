@@ -218,9 +218,15 @@ __device__ __forceinline__ void merge_splits(const DecodeArgs& a, int b, int h0,
 template <int kHeads>
 constexpr int kWavesPerSimd = kHeads == 1 ? 5 : kHeads <= 4 ? 3 : 2;
 
-template <typename Tag, int D, int kHeads, int kSpan, bool kPaged>
+// How cache rows are found: contiguous cache, paged cache with the split's block numbers staged in
+// LDS, or paged cache with the block numbers read from the table in global memory (splits that
+// touch more than kMaxSplitPages blocks).
+enum PageMode { kContiguous = 0, kPagedLds = 1, kPagedGlobal = 2 };
+
+template <typename Tag, int D, int kHeads, int kSpan, int kPageMode>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd<kHeads>)))
 decode_split_kernel(const DecodeArgs a) {
+  constexpr bool kPaged = kPageMode != kContiguous;
   using S = typename Elem<Tag>::storage;
   constexpr int kEPL = 16 / static_cast<int>(sizeof(S));  // elements per 16-byte piece
   constexpr int kLPR = D / kEPL;                           // lanes per cache row
@@ -283,16 +289,20 @@ decode_split_kernel(const DecodeArgs a) {
 
   // Contiguous cache: rows of sequence b at b * bs + key * ss. Paged cache
   // ([num_blocks, page_size, H_kv, D]): key lives in block block_tables[b][key / page_size], row
-  // key % page_size. The split's block numbers are staged in LDS once (clamped to the cache, so a
-  // bad table entry cannot read outside it); LDS reads do not wait behind the rows in flight.
-  __shared__ int page_table[kPaged ? kMaxSplitPages : 1];
+  // key % page_size, block numbers clamped to the pool so a bad table entry cannot read outside
+  // it. kPagedLds stages the split's block numbers in LDS once (the host picks it when every split
+  // touches at most kMaxSplitPages blocks): LDS reads do not wait behind the rows in flight.
+  // kPagedGlobal reads each block number from the table in global memory.
+  __shared__ int page_table[kPageMode == kPagedLds ? kMaxSplitPages : 1];
   int page0 = 0;
-  if constexpr (kPaged) {
+  const int32_t* table_row = nullptr;
+  if constexpr (kPaged) table_row = a.block_tables + static_cast<int64_t>(b) * a.block_tables_stride;
+  if constexpr (kPageMode == kPagedLds) {
     if (k_begin < k_end) {
       page0 = k_begin / a.page_size;
       const int pages = (k_end - 1) / a.page_size - page0 + 1;
-      const int32_t* row = a.block_tables + static_cast<int64_t>(b) * a.block_tables_stride + page0;
-      for (int i = tid; i < pages; i += kThreads) page_table[i] = min(max(row[i], 0), a.num_blocks - 1);
+      for (int i = tid; i < pages; i += kThreads)
+        page_table[i] = min(max(table_row[page0 + i], 0), a.num_blocks - 1);
     }
     __syncthreads();
   }
@@ -301,7 +311,11 @@ decode_split_kernel(const DecodeArgs a) {
   // (block, row) of a key; page sizes that are powers of two (the usual ones) take a shift.
   auto locate = [&](int key, int& block, int& row) {
     const int page = a.page_shift >= 0 ? key >> a.page_shift : key / a.page_size;
-    block = page_table[page - page0];
+    if constexpr (kPageMode == kPagedLds) {
+      block = page_table[page - page0];
+    } else {
+      block = min(max(table_row[page], 0), a.num_blocks - 1);
+    }
     row = key - page * a.page_size;
   };
   auto k_row = [&](int key) -> const S* {
@@ -458,12 +472,15 @@ void launch_split(const DecodeArgs& args, int groups, hipStream_t stream) {
   constexpr int kLPR = D * static_cast<int>(sizeof(typename Elem<Tag>::storage)) / 16;
   if constexpr (kSpan * kLPR <= 64) {
     const dim3 grid(groups / kSpan * args.num_splits);
-    if (args.block_tables != nullptr) {
-      hipLaunchKernelGGL((decode_split_kernel<Tag, D, kHeads, kSpan, true>), grid, dim3(kThreads), 0,
-                         stream, args);
-    } else {
-      hipLaunchKernelGGL((decode_split_kernel<Tag, D, kHeads, kSpan, false>), grid, dim3(kThreads),
-                         0, stream, args);
+    if (args.block_tables == nullptr) {
+      hipLaunchKernelGGL((decode_split_kernel<Tag, D, kHeads, kSpan, kContiguous>), grid,
+                         dim3(kThreads), 0, stream, args);
+    } else if (!args.page_table_global) {
+      hipLaunchKernelGGL((decode_split_kernel<Tag, D, kHeads, kSpan, kPagedLds>), grid,
+                         dim3(kThreads), 0, stream, args);
+    } else if constexpr (kSpan == 1) {  // the rare long-split case: one instantiation per type
+      hipLaunchKernelGGL((decode_split_kernel<Tag, D, kHeads, 1, kPagedGlobal>), grid,
+                         dim3(kThreads), 0, stream, args);
     }
   }
 }

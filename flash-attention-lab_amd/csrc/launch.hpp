@@ -51,6 +51,9 @@ struct DecodeArgs {
   int64_t block_tables_stride;
   int page_size, num_blocks;
   int page_shift;  // log2(page_size) when it is a power of two, else -1
+  // Some split touches more than kMaxSplitPages blocks: block numbers are read from global memory
+  // (and kv_span is 1).
+  int page_table_global;
 };
 
 // Largest split count a decode call may use.

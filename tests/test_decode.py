@@ -261,3 +261,21 @@ def test_paged_decode_in_a_graph():
         eager_again = flash_lab.decode(q, k_pool, v_pool, seq_lens, block_tables=tables)
         torch.cuda.synchronize()
         assert torch.equal(eager_again, eager)
+
+
+@pytest.mark.parametrize("impl", IMPLS)
+def test_paged_splits_longer_than_the_staged_table(impl):
+    # A split touching more than 1024 blocks (decode_inplace: one split; pages of one row) reads
+    # the block numbers from the table in global memory instead of LDS (with one KV head per
+    # workgroup, so the sums run in another order than the contiguous cache's): the reference
+    # rule against the fp64 oracle.
+    gen = torch.Generator(device="cuda").manual_seed(13)
+    q, k_cache, v_cache, seq_lens = make_case((2, 8, 2, 3000, 64, [3000, 2100]), torch.bfloat16, gen)
+    cpu_gen = torch.Generator().manual_seed(14)
+    k_pool, tables = to_paged(k_cache, 1, cpu_gen)
+    cpu_gen = torch.Generator().manual_seed(14)
+    v_pool, _ = to_paged(v_cache, 1, cpu_gen)
+    splits = 1 if impl == "decode_inplace" else 2
+    out, lse = flash_lab.decode(q, k_pool, v_pool, seq_lens, block_tables=tables, impl=impl,
+                                num_splits=splits, return_lse=True)
+    check_decode(out, lse, q, k_cache, v_cache, seq_lens)
