@@ -48,12 +48,6 @@ fl::DType decode_dtype(int32_t dtype) {
   return dtype == FL_DTYPE_BF16 ? fl::DType::bf16 : dtype == FL_DTYPE_F16 ? fl::DType::f16 : fl::DType::f32;
 }
 
-// Largest power of two (at most 128) whose split workgroups all fit on the GPU at once
-// (resident_per_cu per CU; FLASH_LAB_DECODE_WG_PER_CU overrides it for experiments) while each
-// split of the longest possible sequence keeps at least 512 keys. One wave of workgroups that
-// fills the GPU streams the cache with no tail; measured on MI355X at 32K keys, this beat aiming
-// for two or more workgroups per resident slot, and splits of 256 keys (B=1 MHA, 128 splits)
-// lost about 1% to 512-key ones (64 splits).
 // Cache blocks one split may touch at most: its keys (rounded up to the kernel's largest batch of
 // 128 keys) over page_size, plus a partial block at each end.
 int64_t pages_per_split(int max_seqlen, int num_splits, int page_size) {
@@ -61,15 +55,44 @@ int64_t pages_per_split(int max_seqlen, int num_splits, int page_size) {
   return keys / page_size + 2;
 }
 
+// Largest power of two (at most 128) whose split workgroups all fit on the GPU at once
+// (resident_per_cu per CU; FLASH_LAB_DECODE_WG_PER_CU overrides it for experiments) while each
+// split of the longest possible sequence keeps at least 512 keys. One wave of workgroups that
+// fills the GPU streams the cache with no tail; measured on MI355X at 32K keys, this beat aiming
+// for two or more workgroups per resident slot, and splits of 256 keys (B=1 MHA, 128 splits)
+// lost about 1% to 512-key ones (64 splits). When that leaves fewer workgroups than a quarter of
+// the resident slots (a short cache or few sequences and heads, e.g. one 8K-key sequence with 8
+// KV heads: 32 workgroups), splits go down to 64 keys: many short splits beat a few long ones
+// that leave most CUs idle.
 int choose_num_splits(int64_t workgroups, int max_seqlen, int cu_count, int resident_per_cu) {
   if (const char* env = std::getenv("FLASH_LAB_DECODE_WG_PER_CU")) {
     const int v = std::atoi(env);
     if (v >= 1 && v <= 64) resident_per_cu = v;
   }
   const int64_t capacity = static_cast<int64_t>(resident_per_cu) * (cu_count > 0 ? cu_count : 256);
-  int n = 1;
-  while (n < 128 && workgroups * 2 * n <= capacity && max_seqlen / (2 * n) >= 512) n *= 2;
-  return n;
+  auto largest = [&](int min_keys) {
+    int n = 1;
+    while (n < 128 && workgroups * 2 * n <= capacity && max_seqlen / (2 * n) >= min_keys) n *= 2;
+    return n;
+  };
+  const int n = largest(512);
+  return workgroups * n * 4 < capacity ? largest(64) : n;
+}
+
+// Fewest split workgroups for which a workgroup spans several KV heads: below it, one KV head per
+// workgroup gives the GPU more workgroups for the same splits.
+constexpr int64_t kMinSpanWorkgroups = 256;
+
+// KV heads per workgroup for a decode with num_splits splits: the widest span the layout allows
+// that still yields kMinSpanWorkgroups workgroups, else 1. fl_decode_plan and fl_decode both
+// derive it from the same parameters.
+int decode_span(const fl_decode_params* p, const fl::DecodeLayout& layout, int num_splits) {
+  const int group = p->heads / p->heads_kv;
+  for (int s = layout.kv_span; s > 1; s /= 2) {
+    const int64_t wg = static_cast<int64_t>(p->batch) * (p->heads_kv / s) * (group / layout.heads_per_wg);
+    if (wg * num_splits >= kMinSpanWorkgroups) return s;
+  }
+  return 1;
 }
 
 int check_decode_shape(const fl_decode_params* p) {
@@ -181,13 +204,17 @@ int fl_decode_plan(const fl_decode_params* p, int32_t requested_splits, int32_t 
     return fail(FL_ERR_INVALID, "null output pointer");
   const int group = p->heads / p->heads_kv;
   const fl::DecodeLayout layout = fl::decode_layout(decode_dtype(p->dtype), p->head_dim, p->heads_kv, group);
-  const int64_t workgroups = static_cast<int64_t>(p->batch) * (p->heads_kv / layout.kv_span) *
-                             (group / layout.heads_per_wg);
   int n = 1;
-  if (allow_splits) {
-    n = requested_splits > 0
-            ? requested_splits
-            : choose_num_splits(workgroups, p->max_seqlen, cu_count, layout.resident_per_cu);
+  if (allow_splits && requested_splits > 0) {
+    n = requested_splits;
+  } else if (allow_splits) {
+    // The widest span whose workgroups (with the split count it leads to) reach
+    // kMinSpanWorkgroups; else one KV head per workgroup.
+    for (int s = layout.kv_span; s >= 1; s /= 2) {
+      const int64_t wg = static_cast<int64_t>(p->batch) * (p->heads_kv / s) * (group / layout.heads_per_wg);
+      n = choose_num_splits(wg, p->max_seqlen, cu_count, layout.resident_per_cu);
+      if (s == 1 || wg * n >= kMinSpanWorkgroups) break;
+    }
   }
   if (p->block_tables != nullptr && allow_splits && requested_splits == 0) {
     // A paged split stages its block numbers in LDS when they fit: take more splits if one would
@@ -257,7 +284,7 @@ int fl_decode(const fl_decode_params* p, fl_stream_t stream) {
   a.max_seqlen = p->max_seqlen;
   a.num_splits = p->num_splits;
   a.head_chunks = head_chunks;
-  a.kv_span = layout.kv_span;
+  a.kv_span = decode_span(p, layout, p->num_splits);
   a.block_tables = p->block_tables;
   a.block_tables_stride = p->block_tables_stride;
   a.page_size = p->page_size;

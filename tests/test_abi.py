@@ -74,9 +74,12 @@ def test_decode_plan_requested_and_inplace():
         1,
         0,
     )
-    # Short caches keep >= 512 keys per split.
-    assert _hip.decode_plan(1, 8, 8, 128, 1000, torch.bfloat16)[0] == 1
-    assert _hip.decode_plan(1, 8, 8, 128, 1024, torch.bfloat16)[0] == 2
+    # Splits keep >= 512 keys while that leaves enough workgroups; with few workgroups (one
+    # sequence, 8 KV heads) they go down to 64 keys, and a cache under 128 keys is not split.
+    assert _hip.decode_plan(8, 32, 32, 128, 4096, torch.bfloat16)[0] == 8  # 512 keys each
+    assert _hip.decode_plan(1, 8, 8, 128, 1000, torch.bfloat16)[0] == 8  # 125 keys each
+    assert _hip.decode_plan(1, 8, 8, 128, 100, torch.bfloat16)[0] == 1
+    assert _hip.decode_plan(1, 8, 8, 128, 128, torch.bfloat16)[0] == 2
 
 
 def test_decode_plan_rejections():
