@@ -193,14 +193,16 @@ def cu_count(index: int) -> int:
     return torch.cuda.get_device_properties(index).multi_processor_count
 
 
-def _require(cond: bool, message: str) -> None:
+def _require(cond: bool, message: str, *args) -> None:
+    """Raises RuntimeError(message % args) unless cond; the message is only formatted on failure
+    (these checks run on every op call)."""
     if not cond:
-        raise RuntimeError(message)
+        raise RuntimeError(message % args if args else message)
 
 
 def _check_cuda(**tensors: torch.Tensor) -> None:
     for name, x in tensors.items():
-        _require(x.is_cuda, f"{name} must be a CUDA tensor")
+        _require(x.is_cuda, "%s must be a CUDA tensor", name)
 
 
 # ----------------------------------------------------------------------------------------------
@@ -212,7 +214,7 @@ def prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, sof
     and the fl_attention_fwd call."""
     _check_cuda(q=q, k=k, v=v)
     _require(q.dtype in (torch.bfloat16, torch.float16), "attention_mma_pipelined takes bf16 or fp16")
-    _require(k.dtype == q.dtype and v.dtype == q.dtype, f"k and v must have dtype {q.dtype}")
+    _require(k.dtype == q.dtype and v.dtype == q.dtype, "k and v must have dtype %s", q.dtype)
     _require(q.dim() == 4 and k.dim() == 4 and v.dim() == 4, "q, k, v must be [B, S, H, D]")
     _require(k.shape == v.shape, "k and v must have the same shape")
     _require(
@@ -221,7 +223,7 @@ def prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, sof
     )
     _require(q.device == k.device and q.device == v.device, "q, k, v on different devices")
     for name, x in (("q", q), ("k", k), ("v", v)):
-        _require(x.stride(-1) == 1, f"{name} must be contiguous in its last dimension")
+        _require(x.stride(-1) == 1, "%s must be contiguous in its last dimension", name)
     batch, seqlen_q, heads, head_dim = q.shape
     # The kernel needs non-overlapping K and V rows (sequence stride >= head_dim); broadcast or
     # overlapping views, which the reference also accepts, are passed as contiguous copies.
@@ -308,7 +310,8 @@ def decode(q, k_cache, v_cache, seq_lens, softmax_scale: float, num_splits: int,
     _require(q.dtype in DTYPE_CODES, "decode takes bf16, fp16, or fp32")
     _require(
         k_cache.dtype == q.dtype and v_cache.dtype == q.dtype,
-        f"k_cache and v_cache must have dtype {q.dtype}",
+        "k_cache and v_cache must have dtype %s",
+        q.dtype,
     )
     _require(seq_lens.dtype == torch.int32, "seq_lens must have dtype int32")
     _require(q.dim() == 3 and k_cache.dim() == 4, "q must be [B, H, D], caches [B, S_max, H_kv, D]")
@@ -334,31 +337,23 @@ def decode(q, k_cache, v_cache, seq_lens, softmax_scale: float, num_splits: int,
     _require(seq_lens.dim() == 1 and seq_lens.shape[0] == q.shape[0], "seq_lens must be [B]")
     _require(seq_lens.is_contiguous(), "seq_lens must be contiguous")
     for name, x in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
-        _require(x.stride(-1) == 1, f"{name} must be contiguous in its last dimension")
+        _require(x.stride(-1) == 1, "%s must be contiguous in its last dimension", name)
     _require(0 <= num_splits <= 128, "num_splits must be in [0, 128]")
 
     o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty(q.shape[:2], dtype=torch.float32, device=q.device)
     p = _decode_params(q, k_cache, v_cache, seq_lens, o, lse, softmax_scale, block_tables)
-    splits = ctypes.c_int32()
-    ws_bytes = ctypes.c_size_t()
     index = q.device.index if q.device.index is not None else torch.cuda.current_device()
-    _check(
-        LIB.fl_decode_plan(
-            ctypes.byref(p),
-            int(num_splits),
-            int(bool(allow_splits)),
-            cu_count(index),
-            ctypes.byref(splits),
-            ctypes.byref(ws_bytes),
-        )
-    )
-    p.num_splits = splits.value
+    splits, ws_bytes = ctypes.c_int32(), ctypes.c_size_t()
+    _check(LIB.fl_decode_plan(ctypes.byref(p), int(num_splits), int(bool(allow_splits)),
+                              cu_count(index), ctypes.byref(splits), ctypes.byref(ws_bytes)))
+    splits, ws_bytes = splits.value, ws_bytes.value
+    p.num_splits = splits
     workspace = None
-    if ws_bytes.value:
-        workspace = torch.empty(ws_bytes.value // 4, dtype=torch.float32, device=q.device)
+    if ws_bytes:
+        workspace = torch.empty(ws_bytes // 4, dtype=torch.float32, device=q.device)
         p.workspace = workspace.data_ptr()
-        p.workspace_bytes = ws_bytes.value
+        p.workspace_bytes = ws_bytes
     with _on_device(q.device):
         _check(LIB.fl_decode(ctypes.byref(p), _stream(q.device)))
     return o, lse
