@@ -89,7 +89,7 @@ constexpr int64_t kMinSpanWorkgroups = 256;
 int decode_span(const fl_decode_params* p, const fl::DecodeLayout& layout, int num_splits) {
   const int group = p->heads / p->heads_kv;
   for (int s = layout.kv_span; s > 1; s /= 2) {
-    const int64_t wg = static_cast<int64_t>(p->batch) * (p->heads_kv / s) * (group / layout.heads_per_wg);
+    const int64_t wg = static_cast<int64_t>(p->batch) * (p->heads_kv / s) * (group / layout.wg_heads);
     if (wg * num_splits >= kMinSpanWorkgroups) return s;
   }
   return 1;
@@ -203,7 +203,8 @@ int fl_decode_plan(const fl_decode_params* p, int32_t requested_splits, int32_t 
   if (num_splits == nullptr || workspace_bytes == nullptr)
     return fail(FL_ERR_INVALID, "null output pointer");
   const int group = p->heads / p->heads_kv;
-  const fl::DecodeLayout layout = fl::decode_layout(decode_dtype(p->dtype), p->head_dim, p->heads_kv, group);
+  const fl::DecodeLayout layout =
+      fl::decode_layout(decode_dtype(p->dtype), p->head_dim, p->heads_kv, group);
   int n = 1;
   if (allow_splits && requested_splits > 0) {
     n = requested_splits;
@@ -211,7 +212,7 @@ int fl_decode_plan(const fl_decode_params* p, int32_t requested_splits, int32_t 
     // The widest span whose workgroups (with the split count it leads to) reach
     // kMinSpanWorkgroups; else one KV head per workgroup.
     for (int s = layout.kv_span; s >= 1; s /= 2) {
-      const int64_t wg = static_cast<int64_t>(p->batch) * (p->heads_kv / s) * (group / layout.heads_per_wg);
+      const int64_t wg = static_cast<int64_t>(p->batch) * (p->heads_kv / s) * (group / layout.wg_heads);
       n = choose_num_splits(wg, p->max_seqlen, cu_count, layout.resident_per_cu);
       if (s == 1 || wg * n >= kMinSpanWorkgroups) break;
     }
@@ -285,6 +286,7 @@ int fl_decode(const fl_decode_params* p, fl_stream_t stream) {
   a.num_splits = p->num_splits;
   a.head_chunks = head_chunks;
   a.kv_span = decode_span(p, layout, p->num_splits);
+  a.mfma = layout.mfma;
   a.block_tables = p->block_tables;
   a.block_tables_stride = p->block_tables_stride;
   a.page_size = p->page_size;

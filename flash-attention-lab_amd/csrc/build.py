@@ -24,7 +24,7 @@ INCLUDE = REPO / "include"
 BUILD_DIR = CSRC / "_build"
 OUTPUT = PKG_ROOT / "flash_lab" / "libflash_lab_hip.so"
 
-SOURCES = ("abi.hip", "prefill_fwd.hip", "prefill_pp.hip", "decode.hip", "smoke.hip")
+SOURCES = ("abi.hip", "prefill_fwd.hip", "prefill_pp.hip", "decode.hip", "decode_mfma.hip", "smoke.hip")
 ARCH = "gfx950"
 FLAGS = (
     f"--offload-arch={ARCH}",

@@ -27,6 +27,8 @@
 //    (Merging in the split kernel's last workgroup per head group was measured slower: every
 //    workgroup then has to wait for its partials to reach device scope and for an atomic before it
 //    frees its slot, which costs more than the second launch.)
+#include <cstdlib>
+
 #include "gfx950.hpp"
 #include "launch.hpp"
 
@@ -217,11 +219,6 @@ __device__ __forceinline__ void merge_splits(const DecodeArgs& a, int b, int h0,
 // only two waves per SIMD.
 template <int kHeads>
 constexpr int kWavesPerSimd = kHeads == 1 ? 5 : kHeads <= 4 ? 3 : 2;
-
-// How cache rows are found: contiguous cache, paged cache with the split's block numbers staged in
-// LDS, or paged cache with the block numbers read from the table in global memory (splits that
-// touch more than kMaxSplitPages blocks).
-enum PageMode { kContiguous = 0, kPagedLds = 1, kPagedGlobal = 2 };
 
 template <typename Tag, int D, int kHeads, int kSpan, int kPageMode>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd<kHeads>)))
@@ -486,14 +483,19 @@ void launch_split(const DecodeArgs& args, int groups, hipStream_t stream) {
 }
 
 template <typename Tag, int D, int kHeads>
-hipError_t launch_heads(const DecodeArgs& args, hipStream_t stream) {
+hipError_t launch_heads(const DecodeArgs& args, DType dtype, hipStream_t stream) {
   const int groups = args.batch * args.heads_kv * args.head_chunks;
-  switch (args.kv_span) {
-    case 4: launch_split<Tag, D, kHeads, 4>(args, groups, stream); break;
-    case 2: launch_split<Tag, D, kHeads, 2>(args, groups, stream); break;
-    default: launch_split<Tag, D, kHeads, 1>(args, groups, stream); break;
+  hipError_t err = hipSuccess;
+  if (args.mfma) {
+    err = launch_decode_mfma_split(args, dtype, D, stream);
+  } else {
+    switch (args.kv_span) {
+      case 4: launch_split<Tag, D, kHeads, 4>(args, groups, stream); break;
+      case 2: launch_split<Tag, D, kHeads, 2>(args, groups, stream); break;
+      default: launch_split<Tag, D, kHeads, 1>(args, groups, stream); break;
+    }
+    err = hipGetLastError();
   }
-  hipError_t err = hipGetLastError();
   if (err != hipSuccess || args.num_splits == 1) return err;
   hipLaunchKernelGGL((decode_merge_kernel<Tag, D, kHeads>), dim3(groups), dim3(kThreads), 0, stream,
                      args);
@@ -501,29 +503,52 @@ hipError_t launch_heads(const DecodeArgs& args, hipStream_t stream) {
 }
 
 template <typename Tag, int D>
-hipError_t launch_dim(const DecodeArgs& args, int k_heads, hipStream_t stream) {
+hipError_t launch_dim(const DecodeArgs& args, DType dtype, int k_heads, hipStream_t stream) {
   switch (k_heads) {
-    case 1: return launch_heads<Tag, D, 1>(args, stream);
-    case 2: return launch_heads<Tag, D, 2>(args, stream);
-    case 4: return launch_heads<Tag, D, 4>(args, stream);
-    default: return launch_heads<Tag, D, 8>(args, stream);
+    case 1: return launch_heads<Tag, D, 1>(args, dtype, stream);
+    case 2: return launch_heads<Tag, D, 2>(args, dtype, stream);
+    case 4: return launch_heads<Tag, D, 4>(args, dtype, stream);
+    default: return launch_heads<Tag, D, 8>(args, dtype, stream);
   }
 }
 
 template <typename Tag>
-hipError_t launch_type(const DecodeArgs& args, int head_dim, int k_heads, hipStream_t stream) {
-  return head_dim == 64 ? launch_dim<Tag, 64>(args, k_heads, stream)
-                        : launch_dim<Tag, 128>(args, k_heads, stream);
+hipError_t launch_type(const DecodeArgs& args, DType dtype, int head_dim, int k_heads,
+                       hipStream_t stream) {
+  return head_dim == 64 ? launch_dim<Tag, 64>(args, dtype, k_heads, stream)
+                        : launch_dim<Tag, 128>(args, dtype, k_heads, stream);
 }
 
 }  // namespace
 }  // namespace decode
+
+// Smallest GQA group the matrix-core kernel serves (FLASH_LAB_DECODE_MFMA_MIN_GROUP overrides it,
+// read on every call; a value above kMaxDecodeMfmaHeads turns the kernel off).
+int decode_mfma_min_group() {
+  if (const char* env = std::getenv("FLASH_LAB_DECODE_MFMA_MIN_GROUP")) {
+    const int v = std::atoi(env);
+    if (v >= 1) return v;
+  }
+  return 4;
+}
 
 DecodeLayout decode_layout(DType dtype, int head_dim, int heads_kv, int group) {
   DecodeLayout layout{};
   int k = 1;
   while (k < 8 && group % (2 * k) == 0) k *= 2;
   layout.heads_per_wg = k;
+  if (dtype != DType::f32 && group >= decode_mfma_min_group() &&
+      group <= kMaxDecodeMfmaHeads) {
+    // One KV head per workgroup. Two fit a CU (256 registers per lane, 64 KiB of LDS at D = 128),
+    // but one per CU streamed faster (B=8, 8 KV heads, 32K keys: 6.03-6.09 TB/s against
+    // 5.86-5.95 with two; B=1: 3.75-4.0 against 3.3-3.7).
+    layout.mfma = 1;
+    layout.wg_heads = group;
+    layout.kv_span = 1;
+    layout.resident_per_cu = 1;
+    return layout;
+  }
+  layout.wg_heads = k;
   // Lanes per cache row: 16-byte pieces of head_dim elements. A span of s KV heads puts s * lanes
   // per row on one key, which must fit a wave.
   const int lanes_per_row = head_dim * (dtype == DType::f32 ? 4 : 2) / 16;
@@ -543,9 +568,9 @@ DecodeLayout decode_layout(DType dtype, int head_dim, int heads_kv, int group) {
 hipError_t launch_decode(const DecodeArgs& args, DType dtype, int head_dim, hipStream_t stream) {
   const int k_heads = args.group / args.head_chunks;
   switch (dtype) {
-    case DType::bf16: return decode::launch_type<bf16_tag>(args, head_dim, k_heads, stream);
-    case DType::f16: return decode::launch_type<f16_tag>(args, head_dim, k_heads, stream);
-    default: return decode::launch_type<f32_tag>(args, head_dim, k_heads, stream);
+    case DType::bf16: return decode::launch_type<bf16_tag>(args, dtype, head_dim, k_heads, stream);
+    case DType::f16: return decode::launch_type<f16_tag>(args, dtype, head_dim, k_heads, stream);
+    default: return decode::launch_type<f32_tag>(args, dtype, head_dim, k_heads, stream);
   }
 }
 

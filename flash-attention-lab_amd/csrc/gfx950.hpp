@@ -14,6 +14,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace fl {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -135,6 +137,16 @@ __device__ __forceinline__ void buffer_load16_to_lds_asm(u32x4s words, uint32_t 
                : "v"(offset), "s"(m0), "s"(w)
                : "memory", "m0");
 }
+// global_load_lds_dwordx4: the same LDS write pattern (lane l's 16 bytes at lds_addr + 16 l, the
+// address wave-uniform) from a per-lane 64-bit global address, so rows may sit anywhere (no 32-bit
+// offset range, no buffer resource). Issued from inline assembly for the same reason as above.
+__device__ __forceinline__ void global_load16_to_lds_asm(const void* src, uint32_t lds_addr) {
+  const uint32_t m0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_addr)));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(m0)
+               : "memory", "m0");
+}
 // 32-bit LDS address of a __shared__ object.
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
   typedef __attribute__((address_space(3))) const void lds_cvoid;
@@ -176,6 +188,26 @@ __device__ __forceinline__ float group_sum(float x) {
   if constexpr (kLanes >= 32) x += __shfl_xor(x, 16);
   if constexpr (kLanes >= 64) x += __shfl_xor(x, 32);
   return x;
+}
+
+// max(x[l], x[l ^ 32]) and x[l] + x[l ^ 32] on every lane: one v_permlane32_swap (lanes 32-63 of
+// the first result and lanes 0-31 of the second are the other half's values).
+__device__ __forceinline__ float max_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// f(integral_constant<int, i>) for i = I .. N - 1, unrolled at compile time.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
 }
 
 // Butterfly exchange with lane ^ mask through ds_bpermute (works across the 32-lane halves).

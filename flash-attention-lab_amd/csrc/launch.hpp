@@ -54,12 +54,22 @@ struct DecodeArgs {
   // Some split touches more than kMaxSplitPages blocks: block numbers are read from global memory
   // (and kv_span is 1).
   int page_table_global;
+  // The matrix-core split kernel (decode_mfma.hip) serves the call: one workgroup per KV head and
+  // split, with all `group` query heads (kv_span and head_chunks then only shape the merge pass).
+  int mfma;
 };
+
+// How the decode kernels find cache rows: contiguous cache, paged cache with the split's block
+// numbers staged in LDS, or paged cache with the block numbers read from the table in global memory
+// (splits that touch more than kMaxSplitPages blocks).
+enum PageMode { kContiguous = 0, kPagedLds = 1, kPagedGlobal = 2 };
 
 // Largest split count a decode call may use.
 constexpr int kMaxSplits = 128;
 // Most cache blocks one split of a paged decode may touch (its block numbers are staged in LDS).
 constexpr int kMaxSplitPages = 1024;
+// Most query heads per KV head the matrix-core decode kernel serves (its MFMA tile's columns).
+constexpr int kMaxDecodeMfmaHeads = 32;
 
 enum class DType : int { bf16 = 0, f16 = 1, f32 = 2 };
 
@@ -72,16 +82,23 @@ hipError_t launch_prefill(const PrefillArgs& args, DType dtype, int head_dim, hi
 hipError_t launch_prefill_pingpong(const PrefillArgs& args, DType dtype, int head_dim,
                                    hipStream_t stream);
 
-// How decode work is laid out: each workgroup serves heads_per_wg query heads (a power of two
-// dividing the GQA group) of each of kv_span adjacent KV heads, and a CU holds resident_per_cu such
-// workgroups at once (their register budget).
+// How decode work is laid out. The vector kernel (decode.hip): each workgroup serves heads_per_wg
+// query heads (a power of two dividing the GQA group) of each of kv_span adjacent KV heads. The
+// matrix-core kernel (mfma = 1): one KV head and its whole group per workgroup (kv_span 1,
+// wg_heads = group). heads_per_wg is also the merge pass's chunk of heads either way. A CU holds
+// resident_per_cu split workgroups at once (registers or LDS).
 struct DecodeLayout {
   int heads_per_wg;
   int kv_span;
   int resident_per_cu;
+  int mfma;
+  int wg_heads;  // query heads per KV head in one split workgroup
 };
 DecodeLayout decode_layout(DType dtype, int head_dim, int heads_kv, int group);
 hipError_t launch_decode(const DecodeArgs& args, DType dtype, int head_dim, hipStream_t stream);
+// The matrix-core split kernel alone (launch_decode runs it and the merge pass when args.mfma).
+hipError_t launch_decode_mfma_split(const DecodeArgs& args, DType dtype, int head_dim,
+                                    hipStream_t stream);
 
 hipError_t launch_axpy(const float* x, const float* y, float alpha, float* out, int64_t n,
                        hipStream_t stream);

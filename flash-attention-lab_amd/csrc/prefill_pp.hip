@@ -70,15 +70,6 @@ static_assert(kStages == 3 || kStages == 4, "3 or 4 ring stages");
 #define FL_PP_AHEAD 4
 #endif
 
-// f(integral_constant<int, i>) for i = I .. N - 1, unrolled at compile time.
-template <int I, int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    static_for<I + 1, N>(f);
-  }
-}
-
 __device__ __forceinline__ float max_of(const f32x16& x, const f32x16& y) {
   float t[11];
 #pragma unroll
@@ -91,17 +82,6 @@ __device__ __forceinline__ float max_of(const f32x16& x, const f32x16& y) {
   const float u2 = fmaxf(fmaxf(t[6], t[7]), t[8]);
   const float u3 = fmaxf(t[9], t[10]);
   return fmaxf(fmaxf(u0, u1), fmaxf(u2, u3));
-}
-
-// max(x[l], x[l ^ 32]) on every lane: one v_permlane32_swap (lanes 32-63 of the first result and
-// lanes 0-31 of the second are the other half's values).
-__device__ __forceinline__ float max_halves(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float sum_halves(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 __device__ __forceinline__ int xcd_remap(int id, int n) {

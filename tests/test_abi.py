@@ -54,17 +54,33 @@ def test_version():
 
 @pytest.mark.parametrize(
     "batch,heads,heads_kv,expected_splits",
-    # The largest power of two whose workgroups all fit at once, with >= 512 keys per split. MHA:
-    # 4 KV heads per workgroup, 5 resident per CU (1280): 8 x 64 (the 512-key floor) and 64 x 16
-    # workgroups. GQA (4 query heads per KV head): 4 KV heads per workgroup, 3 resident per CU
-    # (768): 16 x 32.
-    [(1, 32, 32, 64), (8, 32, 32, 16), (8, 32, 8, 32)],
+    # The largest power of two whose workgroups all fit at once, with >= 512 keys per split. MHA
+    # (vector kernel): 4 KV heads per workgroup, 5 resident per CU (1280): 8 x 64 (the 512-key
+    # floor) and 64 x 16 workgroups. GQA with 4 query heads per KV head (matrix-core kernel): one
+    # KV head per workgroup, 1 resident per CU (256): 64 x 4.
+    [(1, 32, 32, 64), (8, 32, 32, 16), (8, 32, 8, 4)],
     ids=["B1-MHA", "B8-MHA", "B8-GQA"],
 )
 def test_decode_plan_on_256_cus(batch, heads, heads_kv, expected_splits):
     splits, ws = _hip.decode_plan(batch, heads, heads_kv, 128, 32768, torch.bfloat16)
     assert splits == expected_splits
     assert ws == batch * heads * splits * (128 + 2) * 4
+
+
+def test_decode_plan_routes_by_group(monkeypatch):
+    # Groups of 4 to 32 query heads per KV head (bf16/fp16) go to the matrix-core kernel, one KV
+    # head per workgroup and one workgroup per CU: B=8 with 8 KV heads takes 4 splits (256
+    # workgroups) whatever the group. Smaller groups and fp32 stay on the vector kernel, and
+    # FLASH_LAB_DECODE_MFMA_MIN_GROUP moves the threshold.
+    plan = lambda heads, dtype=torch.bfloat16: _hip.decode_plan(8, heads, 8, 128, 32768, dtype)[0]
+    assert plan(32) == plan(64) == plan(256) == 4  # groups 4, 8, 32
+    assert plan(16) == 32  # group 2: vector kernel, 4 KV heads per workgroup, 3 per CU
+    assert plan(32, torch.float16) == 4
+    assert plan(32, torch.float32) == 16  # 2 KV heads per workgroup, 3 per CU
+    monkeypatch.setenv("FLASH_LAB_DECODE_MFMA_MIN_GROUP", "1000")
+    assert plan(32) == 32
+    monkeypatch.setenv("FLASH_LAB_DECODE_MFMA_MIN_GROUP", "1")
+    assert plan(8) == 4
 
 
 def test_decode_plan_requested_and_inplace():

@@ -54,6 +54,61 @@ def test_matches_reference(impl, dtype, case):
     check_decode(out, lse, q, k_cache, v_cache, seq_lens)
 
 
+# The matrix-core split kernel (bf16/fp16, up to 32 query heads per KV head) serves groups of 4 and
+# more by default. With FLASH_LAB_DECODE_MFMA_MIN_GROUP=1 it takes every group, MHA included, so
+# the shapes above and some larger groups run through it against the oracle.
+MFMA_CASES = CASES + [
+    (2, 64, 8, 3000, 128, [3000, 77]),  # group 8
+    (2, 64, 4, 1500, 128, [1500, 999]),  # group 16
+    (1, 32, 1, 2100, 64, [2100]),  # group 32 (one KV head)
+    (2, 24, 2, 900, 128, [900, 31]),  # group 12
+]
+
+
+@pytest.fixture
+def mfma_everywhere(monkeypatch):
+    monkeypatch.setenv("FLASH_LAB_DECODE_MFMA_MIN_GROUP", "1")
+
+
+@pytest.fixture
+def vector_only(monkeypatch):
+    monkeypatch.setenv("FLASH_LAB_DECODE_MFMA_MIN_GROUP", "1000")
+
+
+@pytest.mark.parametrize("case", MFMA_CASES, ids=lambda c: f"B{c[0]}-H{c[1]}-Hkv{c[2]}-S{c[3]}-D{c[4]}")
+@pytest.mark.parametrize("dtype", DTYPES[:2], ids=lambda d: str(d).removeprefix("torch."))
+@pytest.mark.parametrize("impl", IMPLS)
+def test_mfma_kernel_matches_reference(impl, dtype, case, mfma_everywhere):
+    print(f"decode (matrix cores) {impl} {dtype} {case}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    q, k_cache, v_cache, seq_lens = make_case(case, dtype, gen)
+    out, lse = flash_lab.decode(q, k_cache, v_cache, seq_lens, impl=impl, return_lse=True)
+    check_decode(out, lse, q, k_cache, v_cache, seq_lens)
+
+
+@pytest.mark.parametrize("num_splits", [1, 2, 8, 64, None])
+def test_mfma_kernel_split_counts(num_splits, mfma_everywhere):
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    q, k_cache, v_cache, seq_lens = make_case(
+        (3, 16, 2, 2000, 128, [2000, 40, 777]), torch.bfloat16, gen
+    )
+    out, lse = flash_lab.decode(
+        q, k_cache, v_cache, seq_lens, impl="splitkv", num_splits=num_splits, return_lse=True
+    )
+    check_decode(out, lse, q, k_cache, v_cache, seq_lens)
+
+
+def test_gqa_benchmark_shape_on_the_vector_kernel(vector_only):
+    # B8-GQA at 32K keys on the vector kernel (the matrix-core kernel serves it by default).
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn(8, 1, 32, 128, device="cuda", dtype=torch.bfloat16, generator=gen)
+    k_cache = torch.randn(8, 32768, 8, 128, device="cuda", dtype=torch.bfloat16, generator=gen)
+    v_cache = torch.randn(8, 32768, 8, 128, device="cuda", dtype=torch.bfloat16, generator=gen)
+    seq_lens = torch.full((8,), 32768, device="cuda", dtype=torch.int32)
+    out, lse = flash_lab.decode(q, k_cache, v_cache, seq_lens, return_lse=True)
+    check_decode(out, lse, q, k_cache, v_cache, seq_lens)
+
+
 @pytest.mark.parametrize("num_splits", [1, 2, 8, 64, None])
 def test_splitkv_split_counts(num_splits):
     # More splits than keys leaves some splits empty; they must not disturb the merge.
