@@ -76,7 +76,6 @@ __global__ void __launch_bounds__(kThreads)
     prefill_fwd_kernel(const PrefillArgs a) {
   using E = Elem<Tag>;
   constexpr int kTile = kTileElems<D>;
-  constexpr int kTileBytes = 2 * kTile;
   // Two K and two V tile slots, each its own array: slot addresses are compile-time constants in
   // the unrolled loop below (every LDS read is one per-lane offset register plus an immediate),
   // and the compiler can tell that loads into one slot do not alias reads of another, so it does

@@ -305,7 +305,6 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
       __builtin_amdgcn_s_setprio(0);
 #endif
     };
-    auto no_hook = [](auto) {};
 
     // P(t) from S(t) against the reference point: p = 2^(s scale_log2 + neg_shift), packed (rounded
     // to the input type) as the P V operand; returns the lane's sum of the unrounded probabilities
