@@ -63,8 +63,12 @@ int64_t pages_per_split(int max_seqlen, int num_splits, int page_size) {
 // lost about 1% to 512-key ones (64 splits). When that leaves fewer workgroups than a quarter of
 // the resident slots (a short cache or few sequences and heads, e.g. one 8K-key sequence with 8
 // KV heads: 32 workgroups), splits go down to 64 keys: many short splits beat a few long ones
-// that leave most CUs idle.
-int choose_num_splits(int64_t workgroups, int max_seqlen, int cu_count, int resident_per_cu) {
+// that leave most CUs idle. The matrix-core kernel (one resident workgroup per CU, four 32-key
+// tiles per pass) takes the largest count that fills the CUs with at least 128 keys per split: on
+// one 8,448-key sequence with 8 KV heads, 32 splits of 264 keys took 14.8 us against 17.4 us for
+// 16 of 528, and at 32K keys 32 splits were the fastest too (29.3 us).
+int choose_num_splits(int64_t workgroups, int max_seqlen, int cu_count, int resident_per_cu,
+                      bool mfma) {
   if (const char* env = std::getenv("FLASH_LAB_DECODE_WG_PER_CU")) {
     const int v = std::atoi(env);
     if (v >= 1 && v <= 64) resident_per_cu = v;
@@ -75,6 +79,7 @@ int choose_num_splits(int64_t workgroups, int max_seqlen, int cu_count, int resi
     while (n < 128 && workgroups * 2 * n <= capacity && max_seqlen / (2 * n) >= min_keys) n *= 2;
     return n;
   };
+  if (mfma) return largest(128);
   const int n = largest(512);
   return workgroups * n * 4 < capacity ? largest(64) : n;
 }
@@ -213,7 +218,7 @@ int fl_decode_plan(const fl_decode_params* p, int32_t requested_splits, int32_t 
     // kMinSpanWorkgroups; else one KV head per workgroup.
     for (int s = layout.kv_span; s >= 1; s /= 2) {
       const int64_t wg = static_cast<int64_t>(p->batch) * (p->heads_kv / s) * (group / layout.wg_heads);
-      n = choose_num_splits(wg, p->max_seqlen, cu_count, layout.resident_per_cu);
+      n = choose_num_splits(wg, p->max_seqlen, cu_count, layout.resident_per_cu, layout.mfma != 0);
       if (s == 1 || wg * n >= kMinSpanWorkgroups) break;
     }
   }

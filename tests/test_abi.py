@@ -77,6 +77,10 @@ def test_decode_plan_routes_by_group(monkeypatch):
     assert plan(16) == 32  # group 2: vector kernel, 4 KV heads per workgroup, 3 per CU
     assert plan(32, torch.float16) == 4
     assert plan(32, torch.float32) == 16  # 2 KV heads per workgroup, 3 per CU
+    # Short caches: as many splits as fill the CUs with >= 128 keys each.
+    assert _hip.decode_plan(1, 32, 8, 128, 8448, torch.bfloat16)[0] == 32
+    assert _hip.decode_plan(1, 32, 8, 128, 2048, torch.bfloat16)[0] == 16
+    assert _hip.decode_plan(1, 32, 8, 128, 100, torch.bfloat16)[0] == 1
     monkeypatch.setenv("FLASH_LAB_DECODE_MFMA_MIN_GROUP", "1000")
     assert plan(32) == 32
     monkeypatch.setenv("FLASH_LAB_DECODE_MFMA_MIN_GROUP", "1")
