@@ -523,13 +523,16 @@ hipError_t launch_type(const DecodeArgs& args, DType dtype, int head_dim, int k_
 }  // namespace decode
 
 // Smallest GQA group the matrix-core kernel serves (FLASH_LAB_DECODE_MFMA_MIN_GROUP overrides it,
-// read on every call; a value above kMaxDecodeMfmaHeads turns the kernel off).
-int decode_mfma_min_group() {
+// read on every call; a value above kMaxDecodeMfmaHeads turns the kernel off). Measured at 32K keys,
+// B=8, 8 KV heads: at D = 128 it beats the vector kernel from 4 query heads per KV head (6.18 vs
+// 6.0 TB/s fp16; 2 heads: 6.09 vs 6.38); at D = 64 (128-byte rows) from 8 (5.34 vs 4.1; at 4,
+// 5.35-5.39 vs 5.30-5.63).
+int decode_mfma_min_group(int head_dim) {
   if (const char* env = std::getenv("FLASH_LAB_DECODE_MFMA_MIN_GROUP")) {
     const int v = std::atoi(env);
     if (v >= 1) return v;
   }
-  return 4;
+  return head_dim == 64 ? 8 : 4;
 }
 
 DecodeLayout decode_layout(DType dtype, int head_dim, int heads_kv, int group) {
@@ -537,7 +540,7 @@ DecodeLayout decode_layout(DType dtype, int head_dim, int heads_kv, int group) {
   int k = 1;
   while (k < 8 && group % (2 * k) == 0) k *= 2;
   layout.heads_per_wg = k;
-  if (dtype != DType::f32 && group >= decode_mfma_min_group() &&
+  if (dtype != DType::f32 && group >= decode_mfma_min_group(head_dim) &&
       group <= kMaxDecodeMfmaHeads) {
     // One KV head per workgroup. Two fit a CU (256 registers per lane, 64 KiB of LDS at D = 128),
     // but one per CU streamed faster (B=8, 8 KV heads, 32K keys: 6.03-6.09 TB/s against

@@ -68,15 +68,18 @@ def test_decode_plan_on_256_cus(batch, heads, heads_kv, expected_splits):
 
 
 def test_decode_plan_routes_by_group(monkeypatch):
-    # Groups of 4 to 32 query heads per KV head (bf16/fp16) go to the matrix-core kernel, one KV
-    # head per workgroup and one workgroup per CU: B=8 with 8 KV heads takes 4 splits (256
-    # workgroups) whatever the group. Smaller groups and fp32 stay on the vector kernel, and
-    # FLASH_LAB_DECODE_MFMA_MIN_GROUP moves the threshold.
+    # Groups of 4 to 32 query heads per KV head (bf16/fp16, head_dim 128) go to the matrix-core
+    # kernel, one KV head per workgroup and one workgroup per CU: B=8 with 8 KV heads takes 4
+    # splits (256 workgroups) whatever the group. Smaller groups and fp32 stay on the vector
+    # kernel, and FLASH_LAB_DECODE_MFMA_MIN_GROUP moves the threshold.
     plan = lambda heads, dtype=torch.bfloat16: _hip.decode_plan(8, heads, 8, 128, 32768, dtype)[0]
     assert plan(32) == plan(64) == plan(256) == 4  # groups 4, 8, 32
     assert plan(16) == 32  # group 2: vector kernel, 4 KV heads per workgroup, 3 per CU
     assert plan(32, torch.float16) == 4
     assert plan(32, torch.float32) == 16  # 2 KV heads per workgroup, 3 per CU
+    # head_dim 64 (128-byte rows): from 8 query heads per KV head.
+    assert _hip.decode_plan(8, 32, 8, 64, 32768, torch.bfloat16)[0] == 32
+    assert _hip.decode_plan(8, 64, 8, 64, 32768, torch.bfloat16)[0] == 4
     # Short caches: as many splits as fill the CUs with >= 128 keys each.
     assert _hip.decode_plan(1, 32, 8, 128, 8448, torch.bfloat16)[0] == 32
     assert _hip.decode_plan(1, 32, 8, 128, 2048, torch.bfloat16)[0] == 16
