@@ -3,8 +3,9 @@
 Cases follow the reference's tests/test_decode.py:11-119: three dtypes, GQA groups 1 to 8 (and a
 group of 3), ragged and random lengths, split counts with empty splits, a strided cache carved out
 of a larger allocation, rank-3 queries, bitwise determinism, rejections. Added: the three
-benchmark shapes at 32K keys, split-count invariance within tolerance, and lengths outside the
-cache (clamped on the device instead of read out of bounds).
+benchmark shapes at 32K keys, split-count invariance within tolerance, lengths outside the cache
+(clamped on the device instead of read out of bounds), paged caches, and both split kernels (the
+vector one and the matrix-core one for GQA groups) on every shape, with groups up to 32.
 """
 
 import pytest
@@ -95,6 +96,18 @@ def test_mfma_kernel_split_counts(num_splits, mfma_everywhere):
     out, lse = flash_lab.decode(
         q, k_cache, v_cache, seq_lens, impl="splitkv", num_splits=num_splits, return_lse=True
     )
+    check_decode(out, lse, q, k_cache, v_cache, seq_lens)
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"B{c[0]}-H{c[1]}-Hkv{c[2]}-S{c[3]}-D{c[4]}")
+@pytest.mark.parametrize("dtype", DTYPES[:2], ids=lambda d: str(d).removeprefix("torch."))
+@pytest.mark.parametrize("impl", IMPLS)
+def test_vector_kernel_matches_reference(impl, dtype, case, vector_only):
+    # The groups the matrix-core kernel takes by default, on the vector kernel.
+    print(f"decode (vector kernel) {impl} {dtype} {case}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    q, k_cache, v_cache, seq_lens = make_case(case, dtype, gen)
+    out, lse = flash_lab.decode(q, k_cache, v_cache, seq_lens, impl=impl, return_lse=True)
     check_decode(out, lse, q, k_cache, v_cache, seq_lens)
 
 
@@ -263,9 +276,13 @@ def test_paged_matches_reference(impl, dtype, case):
     check_decode(out, lse, q, k_cache, v_cache, seq_lens)
 
 
+@pytest.mark.parametrize("route", ["auto", "vector"])
 @pytest.mark.parametrize("num_splits", [1, 4, 32])
-def test_paged_equals_contiguous_bitwise(num_splits):
-    # Same keys in the same order per split: a paged cache must give the contiguous cache's bits.
+def test_paged_equals_contiguous_bitwise(num_splits, route, monkeypatch):
+    # Same keys in the same order per split: a paged cache must give the contiguous cache's bits,
+    # on the matrix-core kernel (this group of 4 by default) and on the vector kernel.
+    if route == "vector":
+        monkeypatch.setenv("FLASH_LAB_DECODE_MFMA_MIN_GROUP", "1000")
     gen = torch.Generator(device="cuda").manual_seed(8)
     q, k_cache, v_cache, seq_lens = make_case((3, 32, 8, 3000, 128, [3000, 17, 2048]),
                                               torch.bfloat16, gen)
