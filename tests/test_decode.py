@@ -207,11 +207,16 @@ def test_split_count_changes_results_only_within_tolerance():
         assert normwise_rel(out.cpu(), ref) <= 1e-5, n
 
 
-def test_lengths_outside_the_cache_are_clamped():
+@pytest.mark.parametrize(
+    "case,dtype",
+    [((2, 4, 4, 100, 64, [100, 100]), torch.float32), ((2, 32, 4, 100, 128, [100, 100]), torch.bfloat16)],
+    ids=["vector-fp32", "matrix-core-bf16"],
+)
+def test_lengths_outside_the_cache_are_clamped(case, dtype):
     # seq_lens is not checked on the host; the kernel clamps it to [0, S_max] so that a bad value
     # cannot read outside the cache. A length above S_max behaves as S_max.
     gen = torch.Generator(device="cuda").manual_seed(6)
-    q, k_cache, v_cache, _ = make_case((2, 4, 4, 100, 64, [100, 100]), torch.float32, gen)
+    q, k_cache, v_cache, _ = make_case(case, dtype, gen)
     too_long = torch.tensor([100000, 100], device="cuda", dtype=torch.int32)
     full = torch.tensor([100, 100], device="cuda", dtype=torch.int32)
     torch.testing.assert_close(
