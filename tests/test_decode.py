@@ -281,6 +281,24 @@ def test_paged_matches_reference(impl, dtype, case):
     check_decode(out, lse, q, k_cache, v_cache, seq_lens)
 
 
+@pytest.mark.parametrize("case", PAGED_CASES, ids=lambda c: f"B{c[0]}-H{c[1]}-Hkv{c[2]}-S{c[3]}-D{c[4]}-P{c[6]}")
+@pytest.mark.parametrize("dtype", DTYPES[:2], ids=lambda d: str(d).removeprefix("torch."))
+@pytest.mark.parametrize("impl", IMPLS)
+def test_paged_mfma_kernel_matches_reference(impl, dtype, case, mfma_everywhere):
+    # Every paged case (page sizes 1, 7, 16, 64, 256; head_dim 64 and 128) on the matrix-core kernel.
+    print(f"paged decode (matrix cores) {impl} {dtype} {case}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    *contig, page_size = case
+    q, k_cache, v_cache, seq_lens = make_case(tuple(contig), dtype, gen)
+    cpu_gen = torch.Generator().manual_seed(4)
+    k_pool, tables = to_paged(k_cache, page_size, cpu_gen)
+    cpu_gen = torch.Generator().manual_seed(4)
+    v_pool, _ = to_paged(v_cache, page_size, cpu_gen)
+    out, lse = flash_lab.decode(q, k_pool, v_pool, seq_lens, block_tables=tables, impl=impl,
+                                return_lse=True)
+    check_decode(out, lse, q, k_cache, v_cache, seq_lens)
+
+
 @pytest.mark.parametrize("route", ["auto", "vector"])
 @pytest.mark.parametrize("num_splits", [1, 4, 32])
 def test_paged_equals_contiguous_bitwise(num_splits, route, monkeypatch):
