@@ -50,6 +50,9 @@ DECODE = {
     "B8-GQA": dict(batch=8, heads=32, heads_kv=8, context=32768, head_dim=128),
     # The same cache in 16-row blocks of a pool, in shuffled order (block_tables).
     "B8-GQA-paged16": dict(batch=8, heads=32, heads_kv=8, context=32768, head_dim=128, page_size=16),
+    # The same cache with 8 query heads per KV head (a Llama-70B-like group), not a reference
+    # configuration: the matrix-core decode kernel's case.
+    "B8-GQA8": dict(batch=8, heads=64, heads_kv=8, context=32768, head_dim=128),
 }
 
 
