@@ -67,18 +67,26 @@ int64_t pages_per_split(int max_seqlen, int num_splits, int page_size) {
 // tiles per pass) takes the largest count that fills the CUs with at least 128 keys per split: on
 // one 8,448-key sequence with 8 KV heads, 32 splits of 264 keys took 14.8 us against 17.4 us for
 // 16 of 528, and at 32K keys 32 splits were the fastest too (29.3 us).
-int choose_num_splits(int64_t workgroups, int max_seqlen, int cu_count, int resident_per_cu,
-                      bool mfma) {
+// Largest power of two (at most 128) whose workgroups fit `capacity` and whose splits keep at
+// least min_keys keys.
+int largest_splits(int64_t workgroups, int max_seqlen, int64_t capacity, int min_keys) {
+  int n = 1;
+  while (n < 128 && workgroups * 2 * n <= capacity && max_seqlen / (2 * n) >= min_keys) n *= 2;
+  return n;
+}
+
+int64_t resident_capacity(int cu_count, int resident_per_cu) {
   if (const char* env = std::getenv("FLASH_LAB_DECODE_WG_PER_CU")) {
     const int v = std::atoi(env);
     if (v >= 1 && v <= 64) resident_per_cu = v;
   }
-  const int64_t capacity = static_cast<int64_t>(resident_per_cu) * (cu_count > 0 ? cu_count : 256);
-  auto largest = [&](int min_keys) {
-    int n = 1;
-    while (n < 128 && workgroups * 2 * n <= capacity && max_seqlen / (2 * n) >= min_keys) n *= 2;
-    return n;
-  };
+  return static_cast<int64_t>(resident_per_cu) * (cu_count > 0 ? cu_count : 256);
+}
+
+int choose_num_splits(int64_t workgroups, int max_seqlen, int cu_count, int resident_per_cu,
+                      bool mfma) {
+  const int64_t capacity = resident_capacity(cu_count, resident_per_cu);
+  auto largest = [&](int min_keys) { return largest_splits(workgroups, max_seqlen, capacity, min_keys); };
   if (mfma) return largest(128);
   const int n = largest(512);
   return workgroups * n * 4 < capacity ? largest(64) : n;
@@ -87,6 +95,8 @@ int choose_num_splits(int64_t workgroups, int max_seqlen, int cu_count, int resi
 // Fewest split workgroups for which a workgroup spans several KV heads: below it, one KV head per
 // workgroup gives the GPU more workgroups for the same splits.
 constexpr int64_t kMinSpanWorkgroups = 256;
+// Keys per split the vector kernel prefers when a cache is long enough to fill the GPU with them.
+constexpr int kLongSplitKeys = 2048;
 
 // KV heads per workgroup for a decode with num_splits splits: the widest span the layout allows
 // that still yields kMinSpanWorkgroups workgroups, else 1. fl_decode_plan and fl_decode both
@@ -216,10 +226,30 @@ int fl_decode_plan(const fl_decode_params* p, int32_t requested_splits, int32_t 
   } else if (allow_splits) {
     // The widest span whose workgroups (with the split count it leads to) reach
     // kMinSpanWorkgroups; else one KV head per workgroup.
+    int64_t planned_wg = 0;
     for (int s = layout.kv_span; s >= 1; s /= 2) {
       const int64_t wg = static_cast<int64_t>(p->batch) * (p->heads_kv / s) * (group / layout.wg_heads);
       n = choose_num_splits(wg, p->max_seqlen, cu_count, layout.resident_per_cu, layout.mfma != 0);
-      if (s == 1 || wg * n >= kMinSpanWorkgroups) break;
+      planned_wg = wg * n;
+      if (s == 1 || planned_wg >= kMinSpanWorkgroups) break;
+    }
+    // MHA at head_dim 128, 16-bit (the measured case), with at most two workgroups per CU that
+    // way (few sequences, a long cache): at least 16 splits of at least kLongSplitKeys keys instead, if some span then still
+    // gives every CU a workgroup. B=1, 32 KV heads, 32K keys: 16 splits of 2 KV heads 6.05-6.12
+    // TB/s against 5.99-6.03 for 64 splits of 4; at B=2 and 4 (four workgroups per CU) the longer
+    // splits measured 0.2-0.3% slower, so they are not used there.
+    const int cus = cu_count > 0 ? cu_count : 256;
+    if (!layout.mfma && group == 1 && p->head_dim == 128 && p->dtype != FL_DTYPE_F32 &&
+        planned_wg <= 2 * cus) {
+      const int64_t capacity = resident_capacity(cu_count, layout.resident_per_cu);
+      for (int s = layout.kv_span; s >= 1; s /= 2) {
+        const int64_t wg = static_cast<int64_t>(p->batch) * (p->heads_kv / s) * (group / layout.wg_heads);
+        const int m = largest_splits(wg, p->max_seqlen, capacity, kLongSplitKeys);
+        if (m >= 16 && wg * m >= kMinSpanWorkgroups && p->max_seqlen / m >= kLongSplitKeys) {
+          n = m;
+          break;
+        }
+      }
     }
   }
   if (p->block_tables != nullptr && allow_splits && requested_splits == 0) {

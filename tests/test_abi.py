@@ -55,10 +55,11 @@ def test_version():
 @pytest.mark.parametrize(
     "batch,heads,heads_kv,expected_splits",
     # The largest power of two whose workgroups all fit at once, with >= 512 keys per split. MHA
-    # (vector kernel): 4 KV heads per workgroup, 5 resident per CU (1280): 8 x 64 (the 512-key
-    # floor) and 64 x 16 workgroups. GQA with 4 query heads per KV head (matrix-core kernel): one
-    # KV head per workgroup, 1 resident per CU (256): 64 x 4.
-    [(1, 32, 32, 64), (8, 32, 32, 16), (8, 32, 8, 4)],
+    # (vector kernel): 4 KV heads per workgroup, 5 resident per CU (1280): 64 x 16 workgroups at
+    # B=8; at B=1 that rule gives 8 x 64 (two per CU), and long splits win there: 16 splits of
+    # 2048 keys, 2 KV heads per workgroup (256 workgroups). GQA with 4 query heads per KV head
+    # (matrix-core kernel): one KV head per workgroup, 1 resident per CU (256): 64 x 4.
+    [(1, 32, 32, 16), (8, 32, 32, 16), (8, 32, 8, 4)],
     ids=["B1-MHA", "B8-MHA", "B8-GQA"],
 )
 def test_decode_plan_on_256_cus(batch, heads, heads_kv, expected_splits):
