@@ -63,6 +63,7 @@ MFMA_CASES = CASES + [
     (2, 64, 4, 1500, 128, [1500, 999]),  # group 16
     (1, 32, 1, 2100, 64, [2100]),  # group 32 (one KV head)
     (2, 24, 2, 900, 128, [900, 31]),  # group 12
+    (2, 64, 1, 700, 128, [700, 250]),  # group 64: more than the kernel's 32 columns (vector kernel)
 ]
 
 
