@@ -101,10 +101,6 @@ constexpr int kBufferRsrcWord3 = 0x00020000;  // gfx9-family raw buffer configur
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferRsrcWord3);
 }
-__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int offset) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0));
-}
-
 // buffer_load_dwordx4 ... lds: each lane's 16 bytes go to LDS at `lds_block` + 16 * lane (the
 // block address is wave-uniform); offsets past the resource write zeros.
 __device__ __forceinline__ void buffer_load16_to_lds(__amdgpu_buffer_rsrc_t rsrc, void* lds_block,
@@ -135,16 +131,6 @@ __device__ __forceinline__ void buffer_load16_to_lds_asm(u32x4s words, uint32_t 
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
                :
                : "v"(offset), "s"(m0), "s"(w)
-               : "memory", "m0");
-}
-// global_load_lds_dwordx4: the same LDS write pattern (lane l's 16 bytes at lds_addr + 16 l, the
-// address wave-uniform) from a per-lane 64-bit global address, so rows may sit anywhere (no 32-bit
-// offset range, no buffer resource). Issued from inline assembly for the same reason as above.
-__device__ __forceinline__ void global_load16_to_lds_asm(const void* src, uint32_t lds_addr) {
-  const uint32_t m0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_addr)));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(src), "s"(m0)
                : "memory", "m0");
 }
 // 32-bit LDS address of a __shared__ object.
