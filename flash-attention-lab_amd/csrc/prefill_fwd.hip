@@ -377,14 +377,14 @@ hipError_t launch_typed(const PrefillArgs& args, hipStream_t stream) {
 static_assert(kPrefillBlockM == prefill::kBlockM, "host and kernel tile heights differ");
 static_assert(kPrefillBlockN == prefill::kBlockN, "host and kernel tile widths differ");
 
-// head_dim 128 runs on the ping-pong kernel (prefill_pp.hip); FL_PREFILL_PINGPONG=0 keeps it on this
-// one (for comparisons).
+// head_dim 128 and 64 run on the ping-pong kernel (prefill_pp.hip); FL_PREFILL_PINGPONG=0 keeps
+// them on this one (for comparisons).
 #ifndef FL_PREFILL_PINGPONG
 #define FL_PREFILL_PINGPONG 1
 #endif
 
 // Below this many ping-pong workgroups (256 query rows each, causal blocks paired; one per CU) a
-// D = 128 problem runs on this kernel instead, whose 128-row workgroups (two per CU) spread a
+// problem runs on this kernel instead, whose 128-row workgroups (two per CU) spread a
 // short prompt over more CUs. Measured on MI355X at B=1, H=32, causal: S=1024 takes 24.6 us here
 // against 42.7 us on the ping-pong kernel (64 workgroups), S=2048 ties, S=4096 (256 ping-pong
 // workgroups) is 128 us there against 161 us here. FLASH_LAB_PREFILL_PP_MIN_WG overrides it (read
@@ -396,7 +396,7 @@ int prefill_pp_min_workgroups() {
 
 hipError_t launch_prefill(const PrefillArgs& args, DType dtype, int head_dim, hipStream_t stream) {
   using namespace prefill;
-  if (FL_PREFILL_PINGPONG && head_dim == 128) {
+  if (FL_PREFILL_PINGPONG) {
     const int64_t pp_blocks = (args.seqlen_q + 255) / 256;
     const int64_t pp_items = args.causal ? (pp_blocks + 1) / 2 : pp_blocks;
     if (pp_items * args.batch * args.heads >= prefill_pp_min_workgroups())

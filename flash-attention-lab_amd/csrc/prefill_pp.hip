@@ -3,7 +3,7 @@
 // prefill_tile.hpp); what differs is how the work is laid out over time.
 //
 // Serves the attention_mma_pipelined and attention_mma ops of the reference
-// (csrc/prefill/mma_pipelined.cu:54-183) at head_dim 128; the algorithm (tiling, online softmax
+// (csrc/prefill/mma_pipelined.cu:54-183) at head_dim 128 and 64; the algorithm (tiling, online softmax
 // with the -inf-safe reference point, bottom-right causal mask, 1/l epilogue) follows the
 // reference's definitions (csrc/prefill/mma_tile.cuh:60-174, flash_lab/reference.py:90-152).
 //
@@ -14,6 +14,8 @@
 // softmax wave's phase costs about 5 cycles per instruction (about 9.6 per exponential) and must
 // stay below the MFMA phase's 1024 cycles: everything that is not softmax arithmetic (tile loads,
 // their descriptors) is issued by the MFMA wave, which has idle issue slots while its MFMAs run.
+// At head_dim 64 the MFMA phase is 16 MFMAs (512 cycles) and the softmax phase, the same as at
+// 128, sets the half-period; the kernel still beats the 4-wave kernel of prefill_fwd.hip there.
 //
 //  * Workgroup: 8 waves x 32 query rows = 256 rows of one (batch, head). Waves w and w + 4 share a
 //    SIMD (the dispatcher deals waves to SIMDs with period 4). Group 0 is waves 0-3, group 1 waves
@@ -24,8 +26,8 @@
 //  * K and V tiles (64 keys) stream through a ring of kStages LDS slots each, filled by direct
 //    global -> LDS loads (buffer_load ... lds) issued between the MFMAs of the MFMA phases: group 0
 //    loads K(m + kStages - 1) in half-period 2m, group 1 V(m + kStages - 2) in half-period 2m+1
-//    (4 loads per wave each; a load costs the issuing wave about 70 cycles, which the MFMA phase
-//    has to spare). Each group waits for its own tiles at the end of its softmax phase just before
+//    (4 loads per wave each at D = 128, 2 at D = 64; a load costs the issuing wave about 70
+//    cycles, which the MFMA phase has to spare). Each group waits for its own tiles at the end of its softmax phase just before
 //    they are first read. Loads past the last tile use an empty buffer resource (they write zeros
 //    into a free slot) so every wave issues the same number of loads and the vmcnt accounting is
 //    uniform.
@@ -515,6 +517,10 @@ hipError_t launch_typed(PrefillArgs args, hipStream_t stream) {
 hipError_t launch_prefill_pingpong(const PrefillArgs& args, DType dtype, int head_dim,
                                    hipStream_t stream) {
   using namespace prefill::pp;
+  if (head_dim == 64) {
+    return dtype == DType::bf16 ? launch_typed<bf16_tag, 64>(args, stream)
+                                : launch_typed<f16_tag, 64>(args, stream);
+  }
   if (head_dim != 128) return hipErrorInvalidValue;
   return dtype == DType::bf16 ? launch_typed<bf16_tag, 128>(args, stream)
                               : launch_typed<f16_tag, 128>(args, stream);

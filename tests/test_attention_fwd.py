@@ -54,9 +54,9 @@ def sampled_rows(seqlen, count, seed=0):
     return torch.cat([torch.tensor([0, seqlen - 1]), middle]).sort().values
 
 
-# At head_dim 128 the library runs the 8-wave ping-pong kernel when it fills at least 256
-# workgroups and the 4-wave kernel below that; FLASH_LAB_PREFILL_PP_MIN_WG (read on every call)
-# routes a shape to either one, so both are checked on every shape.
+# The library runs the 8-wave ping-pong kernel when it fills at least 256 workgroups and the
+# 4-wave kernel below that (head_dim 64 and 128 alike); FLASH_LAB_PREFILL_PP_MIN_WG (read on every
+# call) routes a shape to either one, so both are checked on every shape.
 ROUTES = {"auto": None, "pingpong": "0", "wg128": "1000000000"}
 
 
@@ -71,8 +71,6 @@ def route(request, monkeypatch):
 @pytest.mark.parametrize("shape", SHAPES, ids=str)
 @pytest.mark.parametrize("impl,dtype", IMPLS, ids=lambda x: str(x).replace("torch.", ""))
 def test_matches_reference(impl, dtype, shape, causal, route):
-    if route != "auto" and shape[-1] != 128:
-        pytest.skip("head_dim 64 has one kernel")
     print(f"prefill {impl} {dtype} {shape} causal={causal} route={route}", flush=True)
     q, k, v = make_inputs(shape, dtype)
     out, lse = flash_lab.attention(q, k, v, causal=causal, impl=impl, return_lse=True)
@@ -83,8 +81,6 @@ def test_matches_reference(impl, dtype, shape, causal, route):
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 @pytest.mark.parametrize("shape", SLOW_SHAPES, ids=str)
 def test_long_sequences(shape, causal, route):
-    if route != "auto" and shape[-1] != 128:
-        pytest.skip("head_dim 64 has one kernel")
     q, k, v = make_inputs(shape, torch.bfloat16)
     out, lse = flash_lab.attention(q, k, v, causal=causal, return_lse=True)
     check_prefill(out, lse, q, k, v, causal, rows=sampled_rows(shape[1], 256))
