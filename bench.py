@@ -1,25 +1,33 @@
 """Benchmark of the two hot paths on one MI355X; prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--only prefill|decode]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-e2e]
+                    [--only prefill|prefill_causal|decode|<decode name>|e2e_L|copy,...]
 
 Metric: prefill TFLOP/s at (B, H, H_kv, S, D) = (4, 32, 32, 4096, 128) bf16 and
 split-KV decode GB/s at 32K keys. A step is one prefill forward over that batch (non-causal), the
-configuration the metric is quoted on; `value` is its throughput. The causal prefill and the three
+configuration the metric is quoted on; `value` is its throughput. The causal prefill, the three
 decode configurations (B=1 MHA, B=8 MHA, B=8 GQA, 32K keys; B=8 GQA also as a paged cache of
-16-row blocks) are reported under "secondary".
+16-row blocks) and the Llama-3.1-8B-shaped end-to-end run (config L: TTFT and decode ms/step) are
+reported under "secondary".
 
 Inputs are synthetic iid N(0, 1) bf16 from torch.Generator(device="cuda").manual_seed(0), drawn in
 the reference's order (q, k, v; decode q, k_cache, v_cache: reference bench/run.py:122-141), and
 are resident in HBM before timing. Every configuration is checked against the fp64 oracle before
-it is timed (prefill on sampled rows, decode on its first sequence). Prefill FLOPs are
-4 B H S_q S_k D, halved for causal; decode bytes are the K and V bytes read (reference
+it is timed, with the reference's rule (bench/run.py:102-119): prefill on the reference's 256
+sampled query rows of every (batch, head), decode on every sequence in full. A workload that fails
+its check is reported "incorrect", is not timed, and makes the exit status non-zero. Prefill FLOPs
+are 4 B H S_q S_k D, halved for causal; decode bytes are the K and V bytes read (reference
 bench/flops.py:31-57; the reference's variant adding q and o is reported beside them). Decode
 timings zero a 1 GiB buffer before each call so the 256 MB Infinity Cache holds no K/V.
 
 roofline: the dominant kernel's algorithmic FLOPs (or bytes) per launch over its mean duration
 from HIP events recorded on the stream it is launched on, against MI355X peaks (dense bf16 MFMA
-2.5 PFLOP/s, HBM 8 TB/s). cpu_baseline: the oracle (PyTorch fp64 on the host cores) on a bounded
-sample of the prefill workload: 256 query rows of every (batch, head), extrapolated.
+2.5 PFLOP/s, HBM 8 TB/s). cpu_baseline: the reference CPU path (the oracle, a restatement of
+flash_lab.reference: PyTorch fp64 on the host cores, core count stated), timed with perf_counter
+in the same run on bounded samples of each workload: C1 (B=1, H=4, S=256, D=64 fp32 and fp64,
+checked to 1e-5 normwise), the 256-row prefill check causal and non-causal (extrapolated
+TFLOP/s), and the full fp64 decode of D1, D8 and G8 (GB/s of bf16 K+V). Each figure is also
+attached to its GPU workload under "reference_cpu_path".
 """
 
 from __future__ import annotations
@@ -140,16 +148,20 @@ def prefill_inputs(cfg, seed=0):
     return q, k, v
 
 
-def check_prefill(out, q, k, v, causal, rows) -> dict:
-    """The reference's benchmark check (bench/run.py:102-109): error on sampled rows against
-    fp64, at most twice SDPA math's error at the input dtype plus 1e-3."""
+CHECK_ROWS = 256  # query rows of every (batch, head) the prefill check covers (bench/run.py:36)
+FLOOR_BF16 = 1e-3  # the reference's floor for bf16 (bench/run.py:35)
+
+
+def check_prefill(out, qc, kc, vc, causal, rows) -> dict:
+    """The reference's benchmark check (bench/run.py:102-109) on CPU copies of the inputs: error
+    on the sampled rows of every (batch, head) against fp64, at most twice SDPA math's error at
+    the input dtype plus 1e-3, and every output finite."""
     import torch
     import torch.nn.functional as F
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
     from oracle import reference
 
-    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
     ref = reference.attention_rows(qc, kc, vc, rows, causal=causal)
     err = (out.cpu()[:, rows].double() - ref).abs().max().item()
     mask = None
@@ -164,8 +176,9 @@ def check_prefill(out, q, k, v, causal, rows) -> dict:
             attn_mask=mask,
         ).transpose(1, 2)
     err_torch = (base.double() - ref).nan_to_num(0.0).abs().max().item()
-    ok = bool(torch.isfinite(out).all()) and err <= 2 * err_torch + 1e-3
-    return {"max_err_vs_fp64": err, "max_err_torch_vs_fp64": err_torch, "correct": ok}
+    ok = bool(torch.isfinite(out).all()) and err <= 2 * err_torch + FLOOR_BF16
+    return {"max_err_vs_fp64": err, "max_err_torch_vs_fp64": err_torch, "correct": ok,
+            "checked": f"{len(rows)} of {qc.shape[1]} query rows of every (batch, head), all outputs finite"}
 
 
 WARMUP_MIN_S = 0.1  # warm up for at least this long: the clock settles within tens of ms
@@ -220,15 +233,108 @@ def time_op(run, steps: int, warmup: int, flush=None, label: str = "step") -> tu
     return [s.elapsed_time(e) for s, e in zip(starts, ends)], wall
 
 
-def bench_prefill(steps: int, warmup: int, causal: bool) -> dict:
+# ----------------------------------------------------------------------------------------------
+# The reference CPU path: the oracle (PyTorch fp64) on the host cores, timed with perf_counter.
+
+CPU_LEG_BUDGET_S = 6.0  # timed work per CPU leg, beyond its warmup
+CPU_MIN_REPS = 3
+CPU_MAX_REPS = 10
+
+
+def time_cpu(fn, budget_s: float = CPU_LEG_BUDGET_S, warmed_up: bool = False) -> dict:
+    """perf_counter times (ms) of fn() on the host: 2 warmup runs (1 when a run takes over a
+    second, none when the caller has just run the same computation), then runs until budget_s is
+    spent, at least CPU_MIN_REPS and at most CPU_MAX_REPS; median, p10, p90 and the counts."""
+    warmup = 0
+    if not warmed_up:
+        t0 = time.perf_counter()
+        fn()
+        warmup = 1
+        if time.perf_counter() - t0 < 1.0:
+            fn()
+            warmup = 2
+    times = []
+    start = time.perf_counter()
+    while len(times) < CPU_MAX_REPS and (
+        len(times) < CPU_MIN_REPS or time.perf_counter() - start < budget_s
+    ):
+        t0 = time.perf_counter()
+        fn()
+        times.append((time.perf_counter() - t0) * 1e3)
+    return {"ms": summarize(times), "reps": len(times), "warmup": warmup}
+
+
+def cpu_setup() -> dict:
+    """Uses every host core this process may run on; returns the record of what was used."""
+    import torch
+
+    cores = cpu_cores()
+    torch.set_num_threads(cores)
+    return {"cores": cores, "threads": torch.get_num_threads(), "cpu_model": cpu_model(),
+            "heading": f"reference CPU path ({cores} cores)"}
+
+
+def cpu_c1_leg() -> dict:
+    """C1: the CPU configuration of BASELINE.json (B=1, H=H_kv=4, S=256, D=64 fp32, iid N(0,1)
+    from torch.manual_seed(0), non-causal, scale 1/8): the oracle at fp32 and at fp64, and the
+    fp32 output against fp64 at 1e-5 relative (normwise: max |x - ref| / max |ref|)."""
+    import torch
+
+    from oracle import reference
+
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(1, 256, 4, 64) for _ in range(3))
+    out32 = reference.attention(q, k, v, dtype=torch.float32)
+    out64 = reference.attention(q, k, v)
+    rel = ((out32.double() - out64).abs().max() / out64.abs().max()).item()
+    flops = attention_flops(1, 4, 256, 256, 64, causal=False)
+    legs = {}
+    for name, dtype in (("fp32", torch.float32), ("fp64", torch.float64)):
+        t = time_cpu(lambda: reference.attention(q, k, v, dtype=dtype))
+        legs[name] = {**t, "gflops": flops / (t["ms"]["median"] / 1e3) / 1e9}
+    return {"workload": "C1: (B,H,H_kv,S,D)=(1,4,4,256,64) fp32 inputs, non-causal",
+            "fp32": legs["fp32"], "fp64": legs["fp64"], "fp32_vs_fp64_normwise": rel,
+            "correct": rel <= 1e-5}
+
+
+def cpu_prefill_leg(qc, kc, vc, rows, causal) -> dict:
+    """The 256-row fp64 check of the prefill workload (oracle attention_rows, as the reference's
+    bench/run.py:75-109) timed on the host; TFLOP/s extrapolated as 4 B H rows S_k D / t (half
+    of that for causal rows, like the GPU count)."""
+    from oracle import reference
+
+    t = time_cpu(lambda: reference.attention_rows(qc, kc, vc, rows, causal=causal), warmed_up=True)
+    b, s_k, h = qc.shape[0], kc.shape[1], qc.shape[2]
+    flops = attention_flops(b, h, len(rows), s_k, qc.shape[3], causal)
+    return {**t, "tflops": flops / (t["ms"]["median"] / 1e3) / 1e12,
+            "sample": f"oracle fp64 attention_rows, {len(rows)} of {qc.shape[1]} query rows x all "
+                      f"{b * h} (batch, head), {'causal' if causal else 'non-causal'}"}
+
+
+def cpu_decode_leg(qc, kc, vc, lens, kv_bytes) -> dict:
+    """The full fp64 decode (oracle decode: every sequence, every key) timed on the host, in GB/s
+    of the bf16 K+V bytes the GPU reads."""
+    from oracle import reference
+
+    t = time_cpu(lambda: reference.decode(qc, kc, vc, lens), warmed_up=True)
+    return {**t, "gbps": kv_bytes / (t["ms"]["median"] / 1e3) / 1e9,
+            "sample": f"oracle fp64 decode of all {qc.shape[0]} sequences x {kc.shape[1]} keys"}
+
+
+# ----------------------------------------------------------------------------------------------
+# GPU legs
+
+
+def bench_prefill(steps: int, warmup: int, causal: bool, cpu: bool) -> dict:
     import torch
 
     import flash_lab
 
     cfg = PREFILL
     q, k, v = prefill_inputs(cfg)
-    rows = sampled_rows(cfg["seqlen"], 64)
-    check = check_prefill(flash_lab.attention(q, k, v, causal=causal), q, k, v, causal, rows)
+    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+    rows = sampled_rows(cfg["seqlen"], CHECK_ROWS)
+    check = check_prefill(flash_lab.attention(q, k, v, causal=causal), qc, kc, vc, causal, rows)
     if not check["correct"]:
         return {"status": "incorrect", **check}
     times, wall = time_op(lambda: flash_lab.attention(q, k, v, causal=causal), steps, warmup,
@@ -239,7 +345,7 @@ def bench_prefill(steps: int, warmup: int, causal: bool) -> dict:
     stats = summarize(times)
     del q, k, v
     torch.cuda.empty_cache()
-    return {
+    result = {
         "status": "ok",
         "causal": causal,
         "flops": flops,
@@ -251,9 +357,12 @@ def bench_prefill(steps: int, warmup: int, causal: bool) -> dict:
         "frac_of_peak": flops / (mean_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS,
         **check,
     }
+    if cpu:
+        result["reference_cpu_path"] = cpu_prefill_leg(qc, kc, vc, rows, causal)
+    return result
 
 
-def bench_decode(name: str, steps: int, warmup: int, flush) -> dict:
+def bench_decode(name: str, steps: int, warmup: int, flush, cpu: bool) -> dict:
     import torch
 
     import flash_lab
@@ -284,17 +393,19 @@ def bench_decode(name: str, steps: int, warmup: int, flush) -> dict:
     else:
         k_used, v_used = k_cache, v_cache
     out = flash_lab.decode(q, k_used, v_used, seq_lens, block_tables=tables)
-    # Check the first sequence in full against fp64 (the reference checks all of them; one keeps
-    # the CPU side short at 32K keys), with the reference's rule.
-    args = (q[:1].cpu(), k_cache[:1].cpu(), v_cache[:1].cpu(), seq_lens[:1].cpu())
-    ref = reference.decode(*args)
-    plain = reference.decode(*args, dtype=torch.bfloat16)
-    err = (out[:1].cpu().double() - ref).abs().max().item()
-    err_torch = (plain.double() - ref).abs().max().item()
-    ok = bool(torch.isfinite(out).all()) and err <= 2 * err_torch + 1e-3
-    if not ok:
-        return {"status": "incorrect", "max_err_vs_fp64": err, "max_err_torch_vs_fp64": err_torch}
+    # The reference's check (bench/run.py:112-119): every sequence in full against fp64, at most
+    # twice the error of the same op sequence at bf16 plus 1e-3.
+    qc, kc, vc, lc = q.cpu(), k_cache.cpu(), v_cache.cpu(), seq_lens.cpu()
     del k_cache, v_cache
+    ref = reference.decode(qc, kc, vc, lc)
+    plain = reference.decode(qc, kc, vc, lc, dtype=torch.bfloat16)
+    err = (out.cpu().double() - ref).abs().max().item()
+    err_torch = (plain.double() - ref).abs().max().item()
+    ok = bool(torch.isfinite(out).all()) and err <= 2 * err_torch + FLOOR_BF16
+    check = {"max_err_vs_fp64": err, "max_err_torch_vs_fp64": err_torch,
+             "checked": f"all {b} sequences x {ctx} keys x {h} heads, all outputs finite"}
+    if not ok:
+        return {"status": "incorrect", **check}
     times, _ = time_op(lambda: flash_lab.decode(q, k_used, v_used, seq_lens, block_tables=tables),
                        steps, warmup, flush, label=name)
     stats = summarize(times)
@@ -304,7 +415,7 @@ def bench_decode(name: str, steps: int, warmup: int, flush) -> dict:
                                  cu_count_=_hip.cu_count(torch.cuda.current_device()))
     del q, k_used, v_used, tables
     torch.cuda.empty_cache()
-    return {
+    result = {
         "status": "ok",
         "page_size": page_size,
         "kv_bytes": kv,
@@ -319,49 +430,86 @@ def bench_decode(name: str, steps: int, warmup: int, flush) -> dict:
                      "unit": "GB/s", "frac": kv / (mean_ms / 1e3) / 1e9 / PEAK_HBM_GBPS,
                      "per_launch": f"{kv:.4g} B of K+V (every cached row once), mean {mean_ms:.4f} ms "
                                    "for the split and merge kernels"},
-        "max_err_vs_fp64": err,
-        "max_err_torch_vs_fp64": err_torch,
+        **check,
     }
+    # The reference CPU path for the three decode configurations BASELINE.json names (the paged
+    # and 8-head variants are this repo's additions and have the same oracle work as B8-GQA).
+    if cpu and name in ("B1-MHA", "B8-MHA", "B8-GQA"):
+        result["reference_cpu_path"] = cpu_decode_leg(qc, kc, vc, lc, kv)
+    return result
 
 
-# ----------------------------------------------------------------------------------------------
-# CPU baseline: the oracle on the host cores
+# Config L, the reference's end-to-end figures (bench/results/h100-80gb-hbm3/summary-cc64b18.md:
+# 270-271): Llama-3.1-8B with real weights on one H100, B=1, 8,192-token prompt, 256 new tokens.
+E2E_REFERENCE = {"ttft_ms_triton_prefill": 274.8, "ttft_ms_mma_pipelined": 311.7,
+                 "decode_step_ms": 9.58, "hardware": "H100 SXM5, real Llama-3.1-8B weights"}
+E2E_PROMPT = 8192
+E2E_NEW_TOKENS = 256
 
 
-def cpu_baseline(rows_count: int = 256, reps: int = 3) -> dict:
-    """fp64 prefill rows (the oracle's attention_rows) on the host: rows_count query rows of every
-    (batch, head) of the headline shape, non-causal; TFLOP/s extrapolated from the sampled rows."""
+def bench_e2e_l(budget_s: float) -> dict:
+    """Config L through flash_lab.hf: a Llama-3.1-8B-shaped model (32 layers, random bf16 weights
+    seeded on the GPU), B=1, an 8,192-token random prompt, 256 greedy tokens with a static cache
+    and the compiled decode step, as the reference's bench/e2e.py:42-177 times it. The logits at
+    the last prompt position are checked first against an fp32 copy of the weights (at most twice
+    SDPA's bf16 error plus 1e-3). One untimed warmup generation pays for the compilation; the
+    median of the timed runs is reported. Runs stop early (status "budget") if `budget_s` of wall
+    time is spent before the timed runs start."""
     import torch
 
-    from oracle import reference
+    try:
+        import transformers  # noqa: F401
+    except ImportError as exc:
+        return {"status": "skipped", "reason": f"transformers not importable: {exc}"}
+    import e2e
+    import flash_lab.hf
 
-    cores = cpu_cores()
-    torch.set_num_threads(cores)
+    t_start = time.perf_counter()
+    config = {"model": "Llama-3.1-8B-shaped, 32 layers, random bf16 weights (seed 0)",
+              "batch": 1, "prompt_len": E2E_PROMPT, "new_tokens": E2E_NEW_TOKENS,
+              "cache": "static", "decode": "generate() compiled step (fullgraph, HIP graphs)"}
+    name = flash_lab.hf.register()
+    model = e2e.build_model(32, seed=0)
     gen = torch.Generator().manual_seed(0)
-    cfg = PREFILL
-    b, h, hkv, s, d = cfg["batch"], cfg["heads"], cfg["heads_kv"], cfg["seqlen"], cfg["head_dim"]
-    q = torch.randn((b, s, h, d), generator=gen).to(torch.bfloat16)
-    k = torch.randn((b, s, hkv, d), generator=gen).to(torch.bfloat16)
-    v = torch.randn((b, s, hkv, d), generator=gen).to(torch.bfloat16)
-    rows = sampled_rows(s, rows_count)
-    reference.attention_rows(q, k, v, rows[:8])  # warm up allocator and threads
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        reference.attention_rows(q, k, v, rows)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    flops = 4.0 * b * h * len(rows) * s * d
+    ids = torch.randint(0, 128000, (1, E2E_PROMPT), generator=gen).cuda()
+    eos = model.config.eos_token_id
+    want = e2e.reference_logits(model, {E2E_PROMPT: ids}, E2E_PROMPT)[E2E_PROMPT]
+    model.set_attn_implementation("sdpa")
+    err_torch = (e2e.last_logits(model, ids) - want).abs().max().item()
+    model.set_attn_implementation(name)
+    err = (e2e.last_logits(model, ids, E2E_PROMPT + E2E_NEW_TOKENS) - want).abs().max().item()
+    check = {"max_logit_err_vs_fp32": err, "max_logit_err_sdpa_vs_fp32": err_torch}
+    if not err <= 2 * err_torch + FLOOR_BF16:
+        return {"status": "incorrect", "config": config, **check}
+    torch._dynamo.reset()
+    print("# e2e_L: warmup generation (compiles the decode step)", file=sys.stderr, flush=True)
+    e2e.generate(model, ids, E2E_NEW_TOKENS, eos, progress_every=64)
+    warm_s = time.perf_counter() - t_start
+    runs = []
+    for i in range(2):
+        if time.perf_counter() - t_start > budget_s:
+            break
+        print(f"# e2e_L: timed run {i + 1}", file=sys.stderr, flush=True)
+        runs.append(e2e.generate(model, ids, E2E_NEW_TOKENS, eos))
+    del model
+    torch.cuda.empty_cache()
+    if not runs:
+        return {"status": "budget", "config": config, "setup_s": warm_s, **check}
+    ttft = [gaps[0] for _, gaps in runs]
+    steps = [g for _, gaps in runs for g in gaps[1:]]
+    step_ms = summarize(steps)
     return {
-        "value": flops / t / 1e12,
-        "unit": "TFLOP/s",
-        "cores": cores,
-        "kind": "port",
-        "sample": (
-            f"oracle fp64 attention_rows, {len(rows)} of {s} query rows x all {b * h} (batch, head)"
-            f" of (4,32,32,4096,128), non-causal, median of {reps}: {t * 1e3:.0f} ms"
-        ),
-        "cpu_model": cpu_model(),
+        "status": "ok",
+        "config": config,
+        "runs": len(runs),
+        "ttft_ms": statistics.median(ttft),
+        "ttft_ms_runs": ttft,
+        "decode_step_ms": step_ms,
+        "decode_tokens_per_s": 1e3 / step_ms["median"],
+        "reference_h100": E2E_REFERENCE,
+        "setup_s": warm_s,
+        "wall_s": time.perf_counter() - t_start,
+        **check,
     }
 
 
@@ -375,20 +523,23 @@ def parse_args(argv=None):
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--decode-steps", type=int, default=100)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-e2e", action="store_true", help="leave out the config L leg")
+    parser.add_argument("--e2e-budget-s", type=float, default=300.0,
+                        help="wall-time bound of the config L leg before its timed runs")
     parser.add_argument("--trace", action="store_true",
                         help="roctx range per timed step, for rocprofv3 --marker-trace (timings "
                              "then include a synchronize per step)")
     parser.add_argument(
         "--only",
-        help="comma list of workloads to run: prefill, prefill_causal, decode (all three), "
-        f"{', '.join(DECODE)}, copy (a 1 GiB device copy, the calibration of the traffic "
+        help="comma list of workloads to run: prefill, prefill_causal, decode (all of them), "
+        f"{', '.join(DECODE)}, e2e_L, copy (a 1 GiB device copy, the calibration of the traffic "
         "counters); default: all but copy",
     )
     return parser.parse_args(argv)
 
 
-def selected_workloads(only: str | None) -> list[str]:
-    everything = ["prefill", "prefill_causal", *DECODE]
+def selected_workloads(only: str | None, e2e: bool = True) -> list[str]:
+    everything = ["prefill", "prefill_causal", *DECODE] + (["e2e_L"] if e2e else [])
     if not only:
         return everything
     names = []
@@ -396,7 +547,7 @@ def selected_workloads(only: str | None) -> list[str]:
         item = item.strip()
         if item == "decode":
             names += list(DECODE)
-        elif item in everything or item == "copy":
+        elif item in everything or item in ("copy", "e2e_L"):
             names.append(item)
         else:
             raise SystemExit(f"unknown workload {item!r}")
@@ -414,6 +565,15 @@ def bench_copy(steps: int) -> dict:
     mean_ms = sum(times) / len(times)
     return {"status": "ok", "bytes_read": FLUSH_BYTES, "bytes_written": FLUSH_BYTES,
             "mean_ms": mean_ms, "gbps_read_plus_write": 2 * FLUSH_BYTES / (mean_ms / 1e3) / 1e9}
+
+
+def overall_status(headline: dict | None, secondary: dict) -> int:
+    """0 when every workload that ran is ok (a leg skipped for a missing optional dependency or
+    its wall-time bound is not a failure), else 1."""
+    bad = {"incorrect", "error"}
+    if headline is not None and headline.get("status") != "ok":
+        return 1
+    return 1 if any(r.get("status") in bad for r in secondary.values()) else 0
 
 
 def main(argv=None) -> int:
@@ -439,28 +599,44 @@ def main(argv=None) -> int:
 
     global TRACE
     TRACE = args.trace
+    cpu = not args.no_cpu_baseline
+    cpu_record = cpu_setup() if cpu else None
     props = torch.cuda.get_device_properties(0)
-    workloads = selected_workloads(args.only)
+    workloads = selected_workloads(args.only, e2e=not args.no_e2e)
     secondary = {}
     headline = None
+
+    def guarded(label, fn):
+        try:
+            return fn()
+        except Exception as exc:  # recorded and reported, never silently dropped
+            print(f"# {label} failed: {exc!r}", file=sys.stderr, flush=True)
+            return {"status": "error", "error": repr(exc)}
+
     if "prefill" in workloads:
-        headline = bench_prefill(args.steps, args.warmup, causal=False)
+        headline = guarded("prefill", lambda: bench_prefill(args.steps, args.warmup, False, cpu))
         print(f"# prefill non-causal: {json.dumps(headline)}", file=sys.stderr, flush=True)
     if "prefill_causal" in workloads:
-        secondary["prefill_causal"] = bench_prefill(args.steps, args.warmup, causal=True)
+        secondary["prefill_causal"] = guarded(
+            "prefill_causal", lambda: bench_prefill(args.steps, args.warmup, True, cpu))
         print(f"# prefill causal: {json.dumps(secondary['prefill_causal'])}", file=sys.stderr,
               flush=True)
     decodes = [name for name in DECODE if name in workloads]
     if decodes:
         flush = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda")
         for name in decodes:
-            secondary[f"decode_{name}"] = bench_decode(name, args.decode_steps, 10, flush)
+            secondary[f"decode_{name}"] = guarded(
+                name, lambda: bench_decode(name, args.decode_steps, 10, flush, cpu))
             print(f"# decode {name}: {json.dumps(secondary[f'decode_{name}'])}", file=sys.stderr,
                   flush=True)
         del flush
+        torch.cuda.empty_cache()
     if "copy" in workloads:
         secondary["copy"] = bench_copy(args.steps)
         print(f"# copy: {json.dumps(secondary['copy'])}", file=sys.stderr, flush=True)
+    if "e2e_L" in workloads:
+        secondary["e2e_L"] = guarded("e2e_L", lambda: bench_e2e_l(args.e2e_budget_s))
+        print(f"# e2e_L: {json.dumps(secondary['e2e_L'])}", file=sys.stderr, flush=True)
 
     if headline is not None and headline["status"] == "ok":
         value = headline["tflops"]
@@ -478,6 +654,31 @@ def main(argv=None) -> int:
         }
     else:
         value, ms, roofline = 0.0, None, None
+
+    cpu_baseline = None
+    if cpu:
+        legs = {"C1": guarded("cpu C1", cpu_c1_leg)}
+        if headline is not None and "reference_cpu_path" in headline:
+            legs["P_noncausal"] = headline["reference_cpu_path"]
+        for key, label in (("prefill_causal", "P_causal"), ("decode_B1-MHA", "D1"),
+                           ("decode_B8-MHA", "D8"), ("decode_B8-GQA", "G8")):
+            if key in secondary and "reference_cpu_path" in secondary[key]:
+                legs[label] = secondary[key]["reference_cpu_path"]
+        p = legs.get("P_noncausal")
+        cpu_baseline = {
+            "value": p["tflops"] if p else None,
+            "unit": "TFLOP/s",
+            "cores": cpu_record["cores"],
+            "kind": "port",
+            "sample": (
+                f"oracle fp64 attention_rows (restatement of flash_lab.reference), {CHECK_ROWS} of "
+                f"4096 query rows x all 128 (batch, head) of (4,32,32,4096,128), non-causal, "
+                f"median of {p['reps']} runs ({p['ms']['median']:.0f} ms; p10 {p['ms']['p10']:.0f}, "
+                f"p90 {p['ms']['p90']:.0f})" if p else "prefill leg not run"
+            ),
+            **cpu_record,
+            "legs": legs,
+        }
 
     result = {
         "metric": "prefill TFLOP/s @(4,32,32,4096,128) bf16; split-KV decode GB/s @32K KV",
@@ -501,15 +702,13 @@ def main(argv=None) -> int:
             "softmax_scale": 1 / math.sqrt(PREFILL["head_dim"]),
         },
         "roofline": roofline,
-        "cpu_baseline": None,
+        "cpu_baseline": cpu_baseline,
         "secondary": secondary,
         "device": {"name": props.name, "cus": props.multi_processor_count,
                    "arch": getattr(props, "gcnArchName", "")},
     }
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
-    return 0 if headline is None or headline["status"] == "ok" else 1
+    return overall_status(headline, secondary)
 
 
 if __name__ == "__main__":

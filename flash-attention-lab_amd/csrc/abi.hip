@@ -4,16 +4,21 @@
 // The checks restate the reference's op-boundary checks (csrc/common/attn_host.h:18-50,
 // csrc/decode/decode_host.h:18-53, csrc/decode/decode.cu:286-293) on plain pointers and strides;
 // messages keep the reference's wording where its tests match on it.
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
-#include <cstdlib>
 #include <string>
 
 #include "flash_lab_hip.h"
 #include "launch.hpp"
 
 namespace {
+
+// Routing overrides (fl_set_knob); -1 = the built-in rule.
+std::atomic<int> g_knobs[FL_KNOB_COUNT] = {-1, -1, -1};
+constexpr int64_t kKnobMin[FL_KNOB_COUNT] = {0, 1, 1};
+constexpr int64_t kKnobMax[FL_KNOB_COUNT] = {int64_t{1} << 30, int64_t{1} << 20, 64};
 
 thread_local std::string g_last_error;
 
@@ -56,7 +61,7 @@ int64_t pages_per_split(int max_seqlen, int num_splits, int page_size) {
 }
 
 // Largest power of two (at most 128) whose split workgroups all fit on the GPU at once
-// (resident_per_cu per CU; FLASH_LAB_DECODE_WG_PER_CU overrides it for experiments) while each
+// (resident_per_cu per CU; the FL_KNOB_DECODE_WG_PER_CU knob overrides it) while each
 // split of the longest possible sequence keeps at least 512 keys. One wave of workgroups that
 // fills the GPU streams the cache with no tail; measured on MI355X at 32K keys, this beat aiming
 // for two or more workgroups per resident slot, and splits of 256 keys (B=1 MHA, 128 splits)
@@ -76,10 +81,8 @@ int largest_splits(int64_t workgroups, int max_seqlen, int64_t capacity, int min
 }
 
 int64_t resident_capacity(int cu_count, int resident_per_cu) {
-  if (const char* env = std::getenv("FLASH_LAB_DECODE_WG_PER_CU")) {
-    const int v = std::atoi(env);
-    if (v >= 1 && v <= 64) resident_per_cu = v;
-  }
+  const int v = fl::knob(FL_KNOB_DECODE_WG_PER_CU);
+  if (v >= 1) resident_per_cu = v;
   return static_cast<int64_t>(resident_per_cu) * (cu_count > 0 ? cu_count : 256);
 }
 
@@ -127,7 +130,24 @@ int check_decode_shape(const fl_decode_params* p) {
 
 }  // namespace
 
+int fl::knob(int which) {
+  return which >= 0 && which < FL_KNOB_COUNT ? g_knobs[which].load(std::memory_order_relaxed) : -1;
+}
+
 extern "C" {
+
+int fl_set_knob(int32_t knob, int64_t value) {
+  if (knob < 0 || knob >= FL_KNOB_COUNT) return fail(FL_ERR_INVALID, fmt("unknown knob %lld", knob));
+  if (value != -1 && (value < kKnobMin[knob] || value > kKnobMax[knob]))
+    return fail(FL_ERR_INVALID, fmt("knob value %lld out of range", value));
+  g_knobs[knob].store(static_cast<int>(value), std::memory_order_relaxed);
+  return FL_OK;
+}
+
+int64_t fl_get_knob(int32_t knob) {
+  if (knob < 0 || knob >= FL_KNOB_COUNT) return -2;
+  return g_knobs[knob].load(std::memory_order_relaxed);
+}
 
 const char* fl_last_error(void) { return g_last_error.c_str(); }
 

@@ -27,7 +27,6 @@
 //    (Merging in the split kernel's last workgroup per head group was measured slower: every
 //    workgroup then has to wait for its partials to reach device scope and for an atomic before it
 //    frees its slot, which costs more than the second launch.)
-#include <cstdlib>
 
 #include "gfx950.hpp"
 #include "launch.hpp"
@@ -464,22 +463,31 @@ __global__ void __launch_bounds__(kThreads) decode_merge_kernel(const DecodeArgs
   merge_splits<Tag, D, kHeads>(a, b, hkv * a.group + hchunk * kHeads, lds);
 }
 
+// Launches the vector split kernel; a (span, page mode) pair with no instantiation (a span whose
+// rows do not fit a wave, or a span above 1 with block numbers read from global memory, which the
+// host never plans) is reported instead of leaving the outputs unwritten.
 template <typename Tag, int D, int kHeads, int kSpan>
-void launch_split(const DecodeArgs& args, int groups, hipStream_t stream) {
+hipError_t launch_split(const DecodeArgs& args, int groups, hipStream_t stream) {
   constexpr int kLPR = D * static_cast<int>(sizeof(typename Elem<Tag>::storage)) / 16;
   if constexpr (kSpan * kLPR <= 64) {
     const dim3 grid(groups / kSpan * args.num_splits);
     if (args.block_tables == nullptr) {
       hipLaunchKernelGGL((decode_split_kernel<Tag, D, kHeads, kSpan, kContiguous>), grid,
                          dim3(kThreads), 0, stream, args);
-    } else if (!args.page_table_global) {
+      return hipGetLastError();
+    }
+    if (!args.page_table_global) {
       hipLaunchKernelGGL((decode_split_kernel<Tag, D, kHeads, kSpan, kPagedLds>), grid,
                          dim3(kThreads), 0, stream, args);
-    } else if constexpr (kSpan == 1) {  // the rare long-split case: one instantiation per type
+      return hipGetLastError();
+    }
+    if constexpr (kSpan == 1) {  // the rare long-split case: one instantiation per type
       hipLaunchKernelGGL((decode_split_kernel<Tag, D, kHeads, 1, kPagedGlobal>), grid,
                          dim3(kThreads), 0, stream, args);
+      return hipGetLastError();
     }
   }
+  return hipErrorInvalidValue;
 }
 
 template <typename Tag, int D, int kHeads>
@@ -490,11 +498,11 @@ hipError_t launch_heads(const DecodeArgs& args, DType dtype, hipStream_t stream)
     err = launch_decode_mfma_split(args, dtype, D, stream);
   } else {
     switch (args.kv_span) {
-      case 4: launch_split<Tag, D, kHeads, 4>(args, groups, stream); break;
-      case 2: launch_split<Tag, D, kHeads, 2>(args, groups, stream); break;
-      default: launch_split<Tag, D, kHeads, 1>(args, groups, stream); break;
+      case 4: err = launch_split<Tag, D, kHeads, 4>(args, groups, stream); break;
+      case 2: err = launch_split<Tag, D, kHeads, 2>(args, groups, stream); break;
+      case 1: err = launch_split<Tag, D, kHeads, 1>(args, groups, stream); break;
+      default: err = hipErrorInvalidValue; break;
     }
-    err = hipGetLastError();
   }
   if (err != hipSuccess || args.num_splits == 1) return err;
   hipLaunchKernelGGL((decode_merge_kernel<Tag, D, kHeads>), dim3(groups), dim3(kThreads), 0, stream,
@@ -522,16 +530,14 @@ hipError_t launch_type(const DecodeArgs& args, DType dtype, int head_dim, int k_
 }  // namespace
 }  // namespace decode
 
-// Smallest GQA group the matrix-core kernel serves (FLASH_LAB_DECODE_MFMA_MIN_GROUP overrides it,
-// read on every call; a value above kMaxDecodeMfmaHeads turns the kernel off). Measured at 32K keys,
+// Smallest GQA group the matrix-core kernel serves (the FL_KNOB_DECODE_MFMA_MIN_GROUP knob
+// overrides it; a value above kMaxDecodeMfmaHeads turns the kernel off). Measured at 32K keys,
 // B=8, 8 KV heads: at D = 128 it beats the vector kernel from 4 query heads per KV head (6.18 vs
 // 6.0 TB/s fp16; 2 heads: 6.09 vs 6.38); at D = 64 (128-byte rows) from 8 (5.34 vs 4.1; at 4,
 // 5.35-5.39 vs 5.30-5.63).
 int decode_mfma_min_group(int head_dim) {
-  if (const char* env = std::getenv("FLASH_LAB_DECODE_MFMA_MIN_GROUP")) {
-    const int v = std::atoi(env);
-    if (v >= 1) return v;
-  }
+  const int v = knob(FL_KNOB_DECODE_MFMA_MIN_GROUP);
+  if (v >= 1) return v;
   return head_dim == 64 ? 8 : 4;
 }
 

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "flash_lab_hip.h"
+
 namespace fl {
 
 // Prefill problem as the kernels see it. Tensors are [B, S, H, D] with unit stride in D; strides
@@ -72,6 +74,10 @@ constexpr int kMaxSplitPages = 1024;
 constexpr int kMaxDecodeMfmaHeads = 32;
 
 enum class DType : int { bf16 = 0, f16 = 1, f32 = 2 };
+
+// Routing overrides set through fl_set_knob (tests and experiments); -1 means "use the built-in
+// rule". Indexed by enum fl_knob of include/flash_lab_hip.h.
+int knob(int which);
 
 // Rows of queries per prefill workgroup (the kernel's tile height) and keys per tile.
 constexpr int kPrefillBlockM = 128;

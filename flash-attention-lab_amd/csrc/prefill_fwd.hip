@@ -15,7 +15,6 @@
 //  * Work order: the 1-D grid is remapped so each XCD (workgroups are dealt round-robin over the
 //    8 XCDs) runs a contiguous range of (batch, head) pairs and their K/V stay in that XCD's L2.
 //    Within a (batch, head) the causal query blocks run heaviest first.
-#include <cstdlib>
 #include <type_traits>
 
 #include "launch.hpp"
@@ -387,11 +386,11 @@ static_assert(kPrefillBlockN == prefill::kBlockN, "host and kernel tile widths d
 // problem runs on this kernel instead, whose 128-row workgroups (two per CU) spread a
 // short prompt over more CUs. Measured on MI355X at B=1, H=32, causal: S=1024 takes 24.6 us here
 // against 42.7 us on the ping-pong kernel (64 workgroups), S=2048 ties, S=4096 (256 ping-pong
-// workgroups) is 128 us there against 161 us here. FLASH_LAB_PREFILL_PP_MIN_WG overrides it (read
-// on every call, so tests can route one shape to either kernel).
+// workgroups) is 128 us there against 161 us here. The FL_KNOB_PREFILL_PP_MIN_WG knob overrides it
+// (so tests can route one shape to either kernel).
 int prefill_pp_min_workgroups() {
-  if (const char* env = std::getenv("FLASH_LAB_PREFILL_PP_MIN_WG")) return std::atoi(env);
-  return 256;
+  const int v = knob(FL_KNOB_PREFILL_PP_MIN_WG);
+  return v >= 0 ? v : 256;
 }
 
 hipError_t launch_prefill(const PrefillArgs& args, DType dtype, int head_dim, hipStream_t stream) {

@@ -21,6 +21,7 @@ raises ImportError; there is no other code path.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import functools
 import math
@@ -135,6 +136,8 @@ SIGNATURES = {
             ctypes.c_void_p,
         ],
     ),
+    "fl_set_knob": (ctypes.c_int, [ctypes.c_int32, ctypes.c_int64]),
+    "fl_get_knob": (ctypes.c_int64, [ctypes.c_int32]),
     "fl_last_error": (ctypes.c_char_p, []),
     "fl_version": (ctypes.c_char_p, []),
 }
@@ -164,6 +167,31 @@ LIB = load_library()
 def _check(rc: int) -> None:
     if rc != 0:
         raise RuntimeError(LIB.fl_last_error().decode())
+
+
+# Routing overrides of the library (enum fl_knob): test and experiment hooks that pin a call to
+# one of the kernels. None restores the built-in rule.
+KNOBS = {"prefill_pp_min_wg": 0, "decode_mfma_min_group": 1, "decode_wg_per_cu": 2}
+
+
+def set_knob(name: str, value: int | None) -> None:
+    _check(LIB.fl_set_knob(KNOBS[name], -1 if value is None else int(value)))
+
+
+def get_knob(name: str) -> int | None:
+    value = LIB.fl_get_knob(KNOBS[name])
+    return None if value == -1 else value
+
+
+@contextlib.contextmanager
+def knob(name: str, value: int | None):
+    """Sets a routing knob for the duration of the block, then restores its previous value."""
+    previous = get_knob(name)
+    set_knob(name, value)
+    try:
+        yield
+    finally:
+        set_knob(name, previous)
 
 
 def _stream(device: torch.device) -> int:

@@ -145,6 +145,33 @@ int fl_smoke_axpy(const float* x, const float* y, float alpha, float* out, int64
 int fl_mfma_tile_test(const void* a, const void* b, float* c, int32_t k, int32_t trans_b,
                       fl_stream_t stream);
 
+/*
+ * Routing overrides. No counterpart in the reference (its kernel choice is
+ * fixed at build time): a test and experiment hook that pins a call to one
+ * of this library's kernels, so the parity tests can run every shape on
+ * each of them. Process-wide; set it from one thread while no other call is
+ * in flight. value -1 restores the built-in rule; fl_set_knob rejects an
+ * unknown knob or a value outside the knob's range with FL_ERR_INVALID.
+ *   FL_KNOB_PREFILL_PP_MIN_WG      [0, 2^30]: fewest ping-pong workgroups
+ *                                  for which prefill runs the 8-wave kernel
+ *                                  (default 256; 0 = always, 2^30 = never).
+ *   FL_KNOB_DECODE_MFMA_MIN_GROUP  [1, 2^20]: smallest GQA group the
+ *                                  matrix-core decode kernel takes (default
+ *                                  4 at head_dim 128, 8 at 64; above 32 =
+ *                                  never).
+ *   FL_KNOB_DECODE_WG_PER_CU       [1, 64]: resident split workgroups per CU
+ *                                  that fl_decode_plan assumes.
+ */
+enum fl_knob {
+  FL_KNOB_PREFILL_PP_MIN_WG = 0,
+  FL_KNOB_DECODE_MFMA_MIN_GROUP = 1,
+  FL_KNOB_DECODE_WG_PER_CU = 2,
+  FL_KNOB_COUNT = 3
+};
+int fl_set_knob(int32_t knob, int64_t value);
+/* Current value of a knob (-1: the built-in rule), or -2 for an unknown knob. */
+int64_t fl_get_knob(int32_t knob);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* fl_last_error(void);
 

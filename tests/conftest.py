@@ -38,6 +38,18 @@ def _no_tf32():
     torch.backends.cudnn.allow_tf32 = False
 
 
+@pytest.fixture
+def knobs():
+    """The HIP library's routing knobs (flash_lab._hip.set_knob) for one test: every knob is
+    restored to the value it had before the test when the test ends."""
+    from flash_lab import _hip
+
+    saved = {name: _hip.get_knob(name) for name in _hip.KNOBS}
+    yield _hip.set_knob
+    for name, value in saved.items():
+        _hip.set_knob(name, value)
+
+
 @pytest.fixture(scope="session")
 def flash_ops():
     """torch.ops.flash_lab, failing loudly if a GPU is present but the HIP library did not load."""

@@ -49,45 +49,71 @@ def sdpa_math(q, k, v, causal, rows=None, scale=None):
     return out.transpose(1, 2)
 
 
+class PrefillOracle:
+    """The oracle side of the prefill rule for one input: the fp64 output and LSE, PyTorch's own
+    errors at the input dtype, and max |v|. Computed once, it can check several kernels' outputs
+    for the same input. With `rows`, only those query rows (long sequences)."""
+
+    def __init__(self, q, k, v, causal, scale=None, rows=None):
+        self.dtype = q.dtype
+        self.shape = q.shape
+        self.rows = rows
+        qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+        if rows is None:
+            self.ref, self.ref_lse = reference.attention(qc, kc, vc, causal, scale, return_lse=True)
+        else:
+            self.ref, self.ref_lse = reference.attention_rows(
+                qc, kc, vc, rows, causal, scale, return_lse=True
+            )
+        # The math backend returns nan for rows without visible keys; those rows are defined as 0.
+        self.err_torch = (
+            (sdpa_math(qc, kc, vc, causal, rows, scale).double() - self.ref)
+            .nan_to_num(0.0).abs().max().item()
+        )
+        self.vmax = vc.abs().max().item()
+        self.visible = torch.isfinite(self.ref_lse)
+        self.lse_err_torch = None
+        if self.visible.any():
+            if rows is None:
+                _, torch_lse = reference.attention(
+                    qc, kc, vc, causal, scale, return_lse=True, dtype=self.dtype
+                )
+            else:
+                _, torch_lse = reference.attention_rows(
+                    qc, kc, vc, rows, causal, scale, dtype=self.dtype, return_lse=True
+                )
+            self.lse_err_torch = (torch_lse.double() - self.ref_lse)[self.visible].abs().max().item()
+
+    def check(self, out, lse):
+        """Asserts the prefill rule on a kernel's (out, lse); returns (err, err_torch)."""
+        dtype = self.dtype
+        assert out.shape == self.shape and out.dtype == dtype
+        assert lse.shape == (self.shape[0], self.shape[2], self.shape[1]) and lse.dtype == torch.float32
+        out_c, lse_c = out.cpu(), lse.cpu()
+        if self.rows is None:
+            got, got_lse = out_c, lse_c
+        else:
+            got, got_lse = out_c[:, self.rows], lse_c[:, :, self.rows]
+        assert torch.isfinite(got).all()
+        err = (got.double() - self.ref).abs().max().item()
+        err_torch = self.err_torch
+        assert err <= 2 * err_torch + FLOOR[dtype], f"max error {err:.3g}, torch math {err_torch:.3g}"
+        assert err <= GUARD[dtype] * (1 + self.vmax), f"max error {err:.3g} above guard"
+
+        visible = self.visible
+        assert torch.equal(torch.isfinite(got_lse), visible)
+        assert torch.isneginf(got_lse[~visible]).all()
+        if visible.any():
+            lse_err = (got_lse.double() - self.ref_lse)[visible].abs().max().item()
+            assert lse_err <= 2 * self.lse_err_torch + LSE_FLOOR[dtype], (
+                f"lse error {lse_err:.3g}, torch {self.lse_err_torch:.3g}"
+            )
+        return err, err_torch
+
+
 def check_prefill(out, lse, q, k, v, causal, scale=None, rows=None):
     """Asserts the prefill rule; with `rows`, on those query rows only (long sequences)."""
-    dtype = q.dtype
-    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
-    assert out.shape == q.shape and out.dtype == dtype
-    assert lse.shape == (q.shape[0], q.shape[2], q.shape[1]) and lse.dtype == torch.float32
-    out_c, lse_c = out.cpu(), lse.cpu()
-    if rows is None:
-        ref, ref_lse = reference.attention(qc, kc, vc, causal, scale, return_lse=True)
-        got, got_lse = out_c, lse_c
-    else:
-        ref, ref_lse = reference.attention_rows(qc, kc, vc, rows, causal, scale, return_lse=True)
-        got, got_lse = out_c[:, rows], lse_c[:, :, rows]
-    assert torch.isfinite(got).all()
-
-    err = (got.double() - ref).abs().max().item()
-    # The math backend returns nan for rows without visible keys; those rows are defined as 0.
-    err_torch = (
-        (sdpa_math(qc, kc, vc, causal, rows, scale).double() - ref).nan_to_num(0.0).abs().max().item()
-    )
-    assert err <= 2 * err_torch + FLOOR[dtype], f"max error {err:.3g}, torch math {err_torch:.3g}"
-    assert err <= GUARD[dtype] * (1 + vc.abs().max().item()), f"max error {err:.3g} above guard"
-
-    visible = torch.isfinite(ref_lse)
-    assert torch.equal(torch.isfinite(got_lse), visible)
-    assert torch.isneginf(got_lse[~visible]).all()
-    if visible.any():
-        if rows is None:
-            _, torch_lse = reference.attention(qc, kc, vc, causal, scale, return_lse=True, dtype=dtype)
-        else:
-            _, torch_lse = reference.attention_rows(
-                qc, kc, vc, rows, causal, scale, dtype=dtype, return_lse=True
-            )
-        lse_err = (got_lse.double() - ref_lse)[visible].abs().max().item()
-        lse_err_torch = (torch_lse.double() - ref_lse)[visible].abs().max().item()
-        assert lse_err <= 2 * lse_err_torch + LSE_FLOOR[dtype], (
-            f"lse error {lse_err:.3g}, torch {lse_err_torch:.3g}"
-        )
-    return err, err_torch
+    return PrefillOracle(q, k, v, causal, scale, rows).check(out, lse)
 
 
 def check_decode(out, lse, q, k_cache, v_cache, seq_lens, scale=None):

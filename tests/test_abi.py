@@ -16,7 +16,7 @@ HEADER = Path(__file__).resolve().parent.parent / "include" / "flash_lab_hip.h"
 
 def declared_functions() -> set[str]:
     text = HEADER.read_text()
-    return set(re.findall(r"^\s*(?:int|const char\*)\s+(fl_\w+)\s*\(", text, flags=re.M))
+    return set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(fl_\w+)\s*\(", text, flags=re.M))
 
 
 def test_header_declares_the_abi():
@@ -26,6 +26,8 @@ def test_header_declares_the_abi():
         "fl_decode",
         "fl_smoke_axpy",
         "fl_mfma_tile_test",
+        "fl_set_knob",
+        "fl_get_knob",
         "fl_last_error",
         "fl_version",
     }
@@ -48,6 +50,27 @@ def test_struct_layouts_match_the_header():
     assert _hip.DecodeParams.softmax_scale.offset == 160
 
 
+def test_knobs_are_validated_and_restored(knobs):
+    # Routing overrides: known knobs within range only; None (-1) restores the built-in rule.
+    assert _hip.get_knob("prefill_pp_min_wg") is None
+    knobs("prefill_pp_min_wg", 0)
+    assert _hip.get_knob("prefill_pp_min_wg") == 0
+    knobs("decode_wg_per_cu", 64)
+    assert _hip.get_knob("decode_wg_per_cu") == 64
+    for name, bad in (("decode_wg_per_cu", 0), ("decode_wg_per_cu", 65),
+                      ("decode_mfma_min_group", 0), ("prefill_pp_min_wg", -5),
+                      ("prefill_pp_min_wg", (1 << 30) + 1)):
+        with pytest.raises(RuntimeError, match="out of range"):
+            _hip.set_knob(name, bad)
+    assert _hip.LIB.fl_set_knob(7, 1) == 1 and b"unknown knob" in _hip.LIB.fl_last_error()
+    assert _hip.LIB.fl_get_knob(-1) == -2
+    with _hip.knob("decode_mfma_min_group", 1000):
+        assert _hip.get_knob("decode_mfma_min_group") == 1000
+    assert _hip.get_knob("decode_mfma_min_group") is None
+    knobs("decode_wg_per_cu", None)
+    assert _hip.get_knob("decode_wg_per_cu") is None
+
+
 def test_version():
     assert b"gfx950" in _hip.LIB.fl_version()
 
@@ -68,11 +91,11 @@ def test_decode_plan_on_256_cus(batch, heads, heads_kv, expected_splits):
     assert ws == batch * heads * splits * (128 + 2) * 4
 
 
-def test_decode_plan_routes_by_group(monkeypatch):
+def test_decode_plan_routes_by_group(knobs):
     # Groups of 4 to 32 query heads per KV head (bf16/fp16, head_dim 128) go to the matrix-core
     # kernel, one KV head per workgroup and one workgroup per CU: B=8 with 8 KV heads takes 4
     # splits (256 workgroups) whatever the group. Smaller groups and fp32 stay on the vector
-    # kernel, and FLASH_LAB_DECODE_MFMA_MIN_GROUP moves the threshold.
+    # kernel, and the decode_mfma_min_group knob moves the threshold.
     plan = lambda heads, dtype=torch.bfloat16: _hip.decode_plan(8, heads, 8, 128, 32768, dtype)[0]
     assert plan(32) == plan(64) == plan(256) == 4  # groups 4, 8, 32
     assert plan(16) == 32  # group 2: vector kernel, 4 KV heads per workgroup, 3 per CU
@@ -85,9 +108,9 @@ def test_decode_plan_routes_by_group(monkeypatch):
     assert _hip.decode_plan(1, 32, 8, 128, 8448, torch.bfloat16)[0] == 32
     assert _hip.decode_plan(1, 32, 8, 128, 2048, torch.bfloat16)[0] == 16
     assert _hip.decode_plan(1, 32, 8, 128, 100, torch.bfloat16)[0] == 1
-    monkeypatch.setenv("FLASH_LAB_DECODE_MFMA_MIN_GROUP", "1000")
+    knobs("decode_mfma_min_group", 1000)
     assert plan(32) == 32
-    monkeypatch.setenv("FLASH_LAB_DECODE_MFMA_MIN_GROUP", "1")
+    knobs("decode_mfma_min_group", 1)
     assert plan(8) == 4
 
 

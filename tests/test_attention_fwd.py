@@ -2,16 +2,17 @@
 
 Shape list, edge cases and rule follow the reference's tests/test_attention_fwd.py:18-177: ragged
 lengths, S_q != S_k both ways (causal rows without keys), GQA, packed strided inputs, scores of
-order 100, bitwise determinism, rejection of unsupported inputs. Added here: the headline shape
-(4, 32, 32, 4096, 128) checked on sampled rows, and the two tensor-core impl names serving the same
-kernel.
+order 100, bitwise determinism, rejection of unsupported inputs, and the full output of the two
+long shapes in bf16 and fp16. Every shape runs on both kernels of this build (the 8-wave ping-pong
+kernel and the 4-wave one). Added here: the headline shape (4, 32, 32, 4096, 128) checked on the
+reference benchmark's 256 sampled rows, and the two tensor-core impl names serving the same kernel.
 """
 
 import pytest
 import torch
 
 import flash_lab
-from parity import check_prefill
+from parity import PrefillOracle, check_prefill
 
 pytestmark = pytest.mark.gpu
 
@@ -55,15 +56,14 @@ def sampled_rows(seqlen, count, seed=0):
 
 
 # The library runs the 8-wave ping-pong kernel when it fills at least 256 workgroups and the
-# 4-wave kernel below that (head_dim 64 and 128 alike); FLASH_LAB_PREFILL_PP_MIN_WG (read on every
-# call) routes a shape to either one, so both are checked on every shape.
-ROUTES = {"auto": None, "pingpong": "0", "wg128": "1000000000"}
+# 4-wave kernel below that (head_dim 64 and 128 alike); the prefill_pp_min_wg knob routes a shape
+# to either one, so both are checked on every shape.
+ROUTES = {"auto": None, "pingpong": 0, "wg128": 1 << 30}
 
 
 @pytest.fixture(params=list(ROUTES), ids=str)
-def route(request, monkeypatch):
-    if ROUTES[request.param] is not None:
-        monkeypatch.setenv("FLASH_LAB_PREFILL_PP_MIN_WG", ROUTES[request.param])
+def route(request, knobs):
+    knobs("prefill_pp_min_wg", ROUTES[request.param])
     return request.param
 
 
@@ -77,37 +77,63 @@ def test_matches_reference(impl, dtype, shape, causal, route):
     check_prefill(out, lse, q, k, v, causal)
 
 
+# Oracle side of the slow shapes, computed once per (shape, dtype, causal) and shared by the two
+# kernels (the fp64 reference of a 4K or 8K sequence takes seconds on the host).
+_LONG_CASES = {}
+
+
+def _long_case(shape, dtype, causal):
+    key = (shape, dtype, causal)
+    if key not in _LONG_CASES:
+        gen = torch.Generator(device="cuda").manual_seed(sum(shape))
+        batch, seqlen_q, seqlen_k, heads, heads_kv, head_dim = shape
+        q = torch.randn(batch, seqlen_q, heads, head_dim, device="cuda", dtype=dtype, generator=gen)
+        k = torch.randn(batch, seqlen_k, heads_kv, head_dim, device="cuda", dtype=dtype, generator=gen)
+        v = torch.randn(batch, seqlen_k, heads_kv, head_dim, device="cuda", dtype=dtype, generator=gen)
+        _LONG_CASES[key] = ((q, k, v), PrefillOracle(q, k, v, causal))
+    return _LONG_CASES[key]
+
+
 @pytest.mark.slow
+@pytest.mark.parametrize("kernel", ["pingpong", "wg128"])
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("shape", SLOW_SHAPES, ids=str)
-def test_long_sequences(shape, causal, route):
-    q, k, v = make_inputs(shape, torch.bfloat16)
+def test_long_sequences_full_output(shape, dtype, causal, kernel, knobs):
+    # The reference checks the whole output of its long shapes for every dtype
+    # (tests/test_attention_fwd.py:110-118); so does this test, on both kernels.
+    print(f"prefill long {shape} {dtype} causal={causal} kernel={kernel}", flush=True)
+    knobs("prefill_pp_min_wg", ROUTES[kernel])
+    (q, k, v), oracle = _long_case(shape, dtype, causal)
     out, lse = flash_lab.attention(q, k, v, causal=causal, return_lse=True)
-    check_prefill(out, lse, q, k, v, causal, rows=sampled_rows(shape[1], 256))
+    oracle.check(out, lse)
 
 
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 def test_headline_shape_sampled_rows(causal):
-    # (B, H, H_kv, S, D) = (4, 32, 32, 4096, 128) bf16, seeded like the benchmark (q, k, v order).
+    # (B, H, H_kv, S, D) = (4, 32, 32, 4096, 128) bf16, seeded like the benchmark (q, k, v order),
+    # on the 256 sampled rows of the reference's benchmark check (bench/run.py:36, 75-79).
     gen = torch.Generator(device="cuda").manual_seed(0)
     shape = (4, 4096, 32, 128)
     q, k, v = (torch.randn(shape, device="cuda", dtype=torch.bfloat16, generator=gen) for _ in range(3))
     out, lse = flash_lab.attention(q, k, v, causal=causal, return_lse=True)
-    check_prefill(out, lse, q, k, v, causal, rows=sampled_rows(4096, 64))
+    check_prefill(out, lse, q, k, v, causal, rows=sampled_rows(4096, 256))
 
 
 @pytest.mark.parametrize("impl,dtype", IMPLS, ids=lambda x: str(x).replace("torch.", ""))
-def test_large_scores(impl, dtype):
-    # Scores of order 100 overflow exp() unless the running max is subtracted.
+def test_large_scores(impl, dtype, route):
+    # Scores of order 100 overflow exp() unless the running max is subtracted (on each kernel: the
+    # two move their reference points under different rules).
     q, k, v = make_inputs((2, 129, 129, 4, 2, 64), dtype, scale=10.0)
     out, lse = flash_lab.attention(q, k, v, causal=True, impl=impl, return_lse=True)
     check_prefill(out, lse, q, k, v, causal=True)
 
 
+@pytest.mark.parametrize("head_dim", [64, 128])
 @pytest.mark.parametrize("impl,dtype", IMPLS, ids=lambda x: str(x).replace("torch.", ""))
-def test_strided_inputs(impl, dtype):
+def test_strided_inputs(impl, dtype, head_dim, route):
     # q, k, v sliced out of one packed [B, S, 3, H, D] projection: no copies, unusual strides.
-    qkv = torch.randn(2, 77, 3, 4, 64, device="cuda", dtype=dtype)
+    qkv = torch.randn(2, 77, 3, 4, head_dim, device="cuda", dtype=dtype)
     q, k, v = qkv.unbind(dim=2)
     assert not q.is_contiguous()
     out, lse = flash_lab.attention(q, k, v, causal=True, impl=impl, return_lse=True)
@@ -115,7 +141,7 @@ def test_strided_inputs(impl, dtype):
 
 
 @pytest.mark.parametrize("scale", [0.05, 0.5])
-def test_explicit_softmax_scale(scale):
+def test_explicit_softmax_scale(scale, route):
     q, k, v = make_inputs((2, 70, 90, 4, 2, 128), torch.bfloat16)
     out, lse = flash_lab.attention(q, k, v, causal=True, softmax_scale=scale, return_lse=True)
     check_prefill(out, lse, q, k, v, causal=True, scale=scale)

@@ -29,8 +29,10 @@ def test_summarize():
 
 
 def test_workload_selection():
-    assert bench.selected_workloads(None) == ["prefill", "prefill_causal", *bench.DECODE]
+    assert bench.selected_workloads(None) == ["prefill", "prefill_causal", *bench.DECODE, "e2e_L"]
+    assert bench.selected_workloads(None, e2e=False) == ["prefill", "prefill_causal", *bench.DECODE]
     assert bench.selected_workloads("decode,copy") == [*bench.DECODE, "copy"]
+    assert bench.selected_workloads("e2e_L", e2e=False) == ["e2e_L"]
     with pytest.raises(SystemExit):
         bench.selected_workloads("nope")
 
@@ -61,3 +63,31 @@ def test_trace_option_parses():
     args = bench.parse_args(["--trace", "--only", "decode"])
     assert args.trace and args.only == "decode"
     assert not bench.parse_args([]).trace
+
+
+def test_exit_status_fails_on_any_incorrect_workload():
+    ok = {"status": "ok"}
+    assert bench.overall_status(ok, {"a": ok, "e2e_L": {"status": "skipped"}}) == 0
+    assert bench.overall_status(ok, {"e2e_L": {"status": "budget"}}) == 0
+    assert bench.overall_status(ok, {"decode_B8-GQA": {"status": "incorrect"}}) == 1
+    assert bench.overall_status(ok, {"prefill_causal": {"status": "error"}}) == 1
+    assert bench.overall_status({"status": "incorrect"}, {}) == 1
+    assert bench.overall_status(None, {"a": ok}) == 0
+
+
+def test_cpu_timer_respects_reps_and_budget():
+    calls = []
+    t = bench.time_cpu(lambda: calls.append(1), budget_s=0.0)
+    # Two warmup runs (a fast function), then the minimum number of timed runs.
+    assert t["warmup"] == 2 and t["reps"] == bench.CPU_MIN_REPS
+    assert len(calls) == 2 + bench.CPU_MIN_REPS
+    t = bench.time_cpu(lambda: None, budget_s=60.0, warmed_up=True)
+    assert t["warmup"] == 0 and t["reps"] == bench.CPU_MAX_REPS
+    assert set(t["ms"]) == {"median", "p10", "p90", "min"}
+
+
+def test_cpu_c1_leg_meets_the_fp32_rule():
+    # BASELINE.json configs[0], the reference's CPU-runnable case: fp32 within 1e-5 normwise of fp64.
+    leg = bench.cpu_c1_leg()
+    assert leg["correct"] and leg["fp32_vs_fp64_normwise"] <= 1e-5
+    assert leg["fp32"]["reps"] >= bench.CPU_MIN_REPS and leg["fp64"]["gflops"] > 0

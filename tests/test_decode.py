@@ -56,7 +56,7 @@ def test_matches_reference(impl, dtype, case):
 
 
 # The matrix-core split kernel (bf16/fp16, up to 32 query heads per KV head) serves groups of 4 and
-# more by default. With FLASH_LAB_DECODE_MFMA_MIN_GROUP=1 it takes every group, MHA included, so
+# more by default. With the decode_mfma_min_group knob at 1 it takes every group, MHA included, so
 # the shapes above and some larger groups run through it against the oracle.
 MFMA_CASES = CASES + [
     (2, 64, 8, 3000, 128, [3000, 77]),  # group 8
@@ -68,13 +68,13 @@ MFMA_CASES = CASES + [
 
 
 @pytest.fixture
-def mfma_everywhere(monkeypatch):
-    monkeypatch.setenv("FLASH_LAB_DECODE_MFMA_MIN_GROUP", "1")
+def mfma_everywhere(knobs):
+    knobs("decode_mfma_min_group", 1)
 
 
 @pytest.fixture
-def vector_only(monkeypatch):
-    monkeypatch.setenv("FLASH_LAB_DECODE_MFMA_MIN_GROUP", "1000")
+def vector_only(knobs):
+    knobs("decode_mfma_min_group", 1000)
 
 
 @pytest.mark.parametrize("case", MFMA_CASES, ids=lambda c: f"B{c[0]}-H{c[1]}-Hkv{c[2]}-S{c[3]}-D{c[4]}")
@@ -302,11 +302,11 @@ def test_paged_mfma_kernel_matches_reference(impl, dtype, case, mfma_everywhere)
 
 @pytest.mark.parametrize("route", ["auto", "vector"])
 @pytest.mark.parametrize("num_splits", [1, 4, 32])
-def test_paged_equals_contiguous_bitwise(num_splits, route, monkeypatch):
+def test_paged_equals_contiguous_bitwise(num_splits, route, knobs):
     # Same keys in the same order per split: a paged cache must give the contiguous cache's bits,
     # on the matrix-core kernel (this group of 4 by default) and on the vector kernel.
     if route == "vector":
-        monkeypatch.setenv("FLASH_LAB_DECODE_MFMA_MIN_GROUP", "1000")
+        knobs("decode_mfma_min_group", 1000)
     gen = torch.Generator(device="cuda").manual_seed(8)
     q, k_cache, v_cache, seq_lens = make_case((3, 32, 8, 3000, 128, [3000, 17, 2048]),
                                               torch.bfloat16, gen)

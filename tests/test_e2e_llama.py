@@ -2,8 +2,9 @@
 SDPA, after the reference's tests/test_e2e_llama.py:1-123.
 
 The reference runs Llama-3.2-1B-Instruct from the local Hugging Face cache; no checkpoint can be
-downloaded here, so the model is a 2-layer Llama of the same head layout (head_dim 128, GQA 4)
-built from a local config with seeded random weights, and prompts are random token ids. The three
+downloaded here, so the models are built from local configs with seeded random weights and
+prompts are random token ids: a 2-layer Llama of the same head layout (head_dim 128, GQA 4) for
+the quick checks, and the full Llama-3.1-8B shape with an 8,192-token prompt (config L). The three
 checks are the reference's: against an fp32 copy of the same weights, flash_lab's bf16 logits are
 at most twice as far off as SDPA's; greedy generation follows SDPA's tokens until SDPA's own top
 two logits are within two bf16 steps of each other; and with a static cache the decode step
@@ -65,7 +66,7 @@ def prompts():
     return [torch.randint(3, 32000, (1, n), generator=gen).cuda() for n in PROMPT_LENS]
 
 
-def greedy(model, input_ids, impl, cache=None):
+def greedy(model, input_ids, impl, cache=None, new_tokens=None):
     """Greedy tokens and the logits of every step; a static cache also compiles the decode step,
     with fullgraph=True so that any graph break raises."""
     model.set_attn_implementation(impl)
@@ -77,8 +78,8 @@ def greedy(model, input_ids, impl, cache=None):
     out = model.generate(
         input_ids,
         attention_mask=torch.ones_like(input_ids),
-        max_new_tokens=NEW_TOKENS,
-        min_new_tokens=NEW_TOKENS,
+        max_new_tokens=new_tokens or NEW_TOKENS,
+        min_new_tokens=new_tokens or NEW_TOKENS,
         do_sample=False,
         temperature=None,
         top_p=None,
@@ -139,3 +140,42 @@ def test_static_cache_decode_compiles_in_one_graph(model, prompts, sdpa_runs):
     for p, reference in zip(prompts, sdpa_runs, strict=True):
         cache.reset()
         assert_follows(greedy(model, p, NAME, cache), reference)
+
+
+# Config L at full size: the Llama-3.1-8B shape (32 layers, hidden
+# 4096, 32 query / 8 KV heads of 128, MLP 14336, vocab 128256, RoPE theta 5e5) with random bf16
+# weights, B=1 and an 8,192-token random prompt. The reference checks its end-to-end model with
+# the same two rules (tests/test_e2e_llama.py:94-135, bench/e2e.py:76-177): logits at the last
+# prompt position at most twice as far from an fp32 copy of the weights as SDPA's, and greedy
+# tokens from the compiled static-cache decode step that follow SDPA's up to a near-tie.
+L_PROMPT = 8192
+L_NEW_TOKENS = 24
+
+
+@pytest.mark.timeout(900)
+def test_config_l_llama_8b_shape():
+    import e2e
+
+    print("e2e L: building the 32-layer model", flush=True)
+    name = flash_lab.hf.register()
+    model = e2e.build_model(32, seed=0)
+    ids = torch.randint(0, 128000, (1, L_PROMPT), generator=torch.Generator().manual_seed(0)).cuda()
+    print("e2e L: fp32 reference logits", flush=True)
+    want = e2e.reference_logits(model, {L_PROMPT: ids}, L_PROMPT)[L_PROMPT]
+    model.set_attn_implementation("sdpa")
+    err_sdpa = (e2e.last_logits(model, ids) - want).abs().max().item()
+    model.set_attn_implementation(name)
+    err = (e2e.last_logits(model, ids, L_PROMPT + L_NEW_TOKENS) - want).abs().max().item()
+    print(f"e2e L: logit error {err:.4g} (sdpa {err_sdpa:.4g})", flush=True)
+    assert err <= 2 * err_sdpa + 1e-3, (err, err_sdpa)
+
+    print("e2e L: sdpa greedy tokens", flush=True)
+    reference = greedy(model, ids, "sdpa", new_tokens=L_NEW_TOKENS)
+    print("e2e L: compiled static-cache decode", flush=True)
+    torch._dynamo.reset()
+    cache = transformers.StaticCache(config=model.config, max_cache_len=L_PROMPT + L_NEW_TOKENS)
+    step = assert_follows(greedy(model, ids, name, cache, new_tokens=L_NEW_TOKENS), reference)
+    print(f"e2e L: tokens follow sdpa (first difference: {step})", flush=True)
+    del model, cache
+    torch._dynamo.reset()
+    torch.cuda.empty_cache()

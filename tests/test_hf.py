@@ -50,8 +50,11 @@ def test_register_with_transformers():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("kernel", [None, 0, 1 << 30], ids=["auto", "pingpong", "wg128"])
 @pytest.mark.parametrize("prefill_impl", ["auto", "mma_pipelined"])
-def test_prefill_reads_only_the_valid_cache_rows(prefill_impl):
+def test_prefill_reads_only_the_valid_cache_rows(prefill_impl, kernel, knobs):
+    # transformers' [B, H, S, D] cache arrives as transposed views, read in place by either kernel.
+    knobs("prefill_pp_min_wg", kernel)
     q, k, v = hf_inputs(2, 77, 200, 8, 2, 128, device="cuda")
     k[:, :, :77].normal_()
     v[:, :, :77].normal_()
