@@ -93,7 +93,7 @@ class StepClock:
         self.times.append(time.perf_counter())
         n = len(self.times) - 1
         if self.progress_every and n and n % self.progress_every == 0:
-            print(f"  step {n}", flush=True)
+            print(f"  step {n}", file=sys.stderr, flush=True)
 
     def end(self):
         pass
