@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "flash_lab_hip.h"
@@ -133,6 +134,128 @@ int check_decode_shape(const fl_decode_params* p) {
 int fl::knob(int which) {
   return which >= 0 && which < FL_KNOB_COUNT ? g_knobs[which].load(std::memory_order_relaxed) : -1;
 }
+
+namespace {
+
+// Checks, parameter derivation and launch of a decode call whose split workspace (used when
+// num_splits > 1) is `workspace`, `workspace_bytes` long: the caller's (fl_decode) or the
+// library's scratch array (fl_decode_noalloc).
+int decode_call(const fl_decode_params* p, float* workspace, size_t workspace_bytes,
+                fl_stream_t stream) {
+  if (int rc = check_decode_shape(p)) return rc;
+  if (!p->q || !p->k_cache || !p->v_cache || !p->o || !p->lse || !p->seq_lens)
+    return fail(FL_ERR_INVALID, "null tensor pointer");
+  if (!valid_scale(p->softmax_scale)) return fail(FL_ERR_INVALID, "softmax_scale must be positive");
+  if (p->num_splits < 1 || p->num_splits > fl::kMaxSplits)
+    return fail(FL_ERR_INVALID, "num_splits must be in [1, 128]");
+  const int eb = elem_bytes(p->dtype);
+  if (!rows_16_byte(p->q, eb, p->batch, p->q_batch_stride, p->heads, p->q_head_stride, 1, 0))
+    return fail(FL_ERR_INVALID, "q must have 16-byte aligned rows");
+  // Cache dimensions: [B, S_max] rows, or [num_blocks, page_size] for a paged cache.
+  const int64_t outer = p->block_tables != nullptr ? p->num_blocks : p->batch;
+  const int64_t rows = p->block_tables != nullptr ? p->page_size : p->max_seqlen;
+  if (!rows_16_byte(p->k_cache, eb, outer, p->k_batch_stride, rows, p->k_seq_stride, p->heads_kv,
+                    p->k_head_stride))
+    return fail(FL_ERR_INVALID, "k_cache must have 16-byte aligned rows (data pointer and strides)");
+  if (!rows_16_byte(p->v_cache, eb, outer, p->v_batch_stride, rows, p->v_seq_stride, p->heads_kv,
+                    p->v_head_stride))
+    return fail(FL_ERR_INVALID, "v_cache must have 16-byte aligned rows (data pointer and strides)");
+  if (!aligned(p->o, eb) || !aligned(p->lse, 4) || !aligned(p->seq_lens, 4))
+    return fail(FL_ERR_INVALID, "o, lse and seq_lens must be aligned to their element size");
+  if (p->block_tables != nullptr && !aligned(p->block_tables, 4))
+    return fail(FL_ERR_INVALID, "block_tables must be 4-byte aligned");
+
+  const int group = p->heads / p->heads_kv;
+  const fl::DType dt = decode_dtype(p->dtype);
+  const fl::DecodeLayout layout = fl::decode_layout(dt, p->head_dim, p->heads_kv, group);
+  const int head_chunks = group / layout.heads_per_wg;
+  const int64_t blocks = static_cast<int64_t>(p->batch) * p->heads_kv * head_chunks * p->num_splits;
+  if (blocks > (int64_t{1} << 24) || static_cast<int64_t>(p->batch) * p->heads > (int64_t{1} << 24))
+    return fail(FL_ERR_INVALID, "batch * heads too large");
+
+  fl::DecodeArgs a{};
+  a.q = p->q;
+  a.k = p->k_cache;
+  a.v = p->v_cache;
+  a.o = p->o;
+  a.lse = p->lse;
+  a.seq_lens = p->seq_lens;
+  a.q_bs = p->q_batch_stride;
+  a.q_hs = p->q_head_stride;
+  a.k_bs = p->k_batch_stride;
+  a.k_ss = p->k_seq_stride;
+  a.k_hs = p->k_head_stride;
+  a.v_bs = p->v_batch_stride;
+  a.v_ss = p->v_seq_stride;
+  a.v_hs = p->v_head_stride;
+  a.o_bs = p->o_batch_stride;
+  a.o_hs = p->o_head_stride;
+  a.batch = p->batch;
+  a.heads = p->heads;
+  a.heads_kv = p->heads_kv;
+  a.group = group;
+  a.max_seqlen = p->max_seqlen;
+  a.num_splits = p->num_splits;
+  a.head_chunks = head_chunks;
+  a.kv_span = decode_span(p, layout, p->num_splits);
+  a.mfma = layout.mfma;
+  a.block_tables = p->block_tables;
+  a.block_tables_stride = p->block_tables_stride;
+  a.page_size = p->page_size;
+  a.num_blocks = p->num_blocks;
+  a.page_table_global =
+      p->block_tables != nullptr &&
+      pages_per_split(p->max_seqlen, p->num_splits, p->page_size) > fl::kMaxSplitPages;
+  if (a.page_table_global) a.kv_span = 1;
+  a.page_shift = -1;
+  for (int s = 0; s < 31; ++s)
+    if (p->page_size == (1 << s)) a.page_shift = s;
+  a.scale_log2 = static_cast<float>(p->softmax_scale * 1.4426950408889634);
+  if (p->num_splits > 1) {
+    const size_t need =
+        static_cast<size_t>(p->batch) * p->heads * p->num_splits * (p->head_dim + 2) * sizeof(float);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(FL_ERR_INVALID, "decode workspace is missing or smaller than fl_decode_plan reports");
+    if (!aligned(workspace, 16)) return fail(FL_ERR_INVALID, "decode workspace must be 16-byte aligned");
+    a.partial_o = workspace;
+    a.partial_ml = workspace + static_cast<size_t>(p->batch) * p->heads * p->num_splits * p->head_dim;
+  }
+  const hipError_t err = fl::launch_decode(a, dt, p->head_dim, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(FL_ERR_LAUNCH, std::string("decode launch: ") + hipGetErrorString(err));
+  return FL_OK;
+}
+
+// The split workspace of fl_decode_noalloc: a file-scope device array, one copy per GPU (each GPU
+// the library runs on holds it until the process ends). In host code `scratch` is a host-side
+// stand-in for the array, not its device address: the address comes from hipGetSymbolAddress,
+// looked up once per device with that device current, and only that address is passed on.
+constexpr size_t kScratchBytes = size_t{16} << 20;
+static __device__ __attribute__((aligned(256))) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch array.
+int scratch_for_current_device(float** out) {
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return fail(FL_ERR_LAUNCH, std::string("hipGetDevice: ") + hipGetErrorString(err));
+  if (device < 0 || device >= kMaxDevices)
+    return fail(FL_ERR_INVALID, fmt("device %lld is beyond the scratch table", device));
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr)
+      return fail(FL_ERR_LAUNCH, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(err));
+    g_scratch_ptr[device] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[device];
+  return FL_OK;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -285,88 +408,25 @@ int fl_decode_plan(const fl_decode_params* p, int32_t requested_splits, int32_t 
 }
 
 int fl_decode(const fl_decode_params* p, fl_stream_t stream) {
+  if (p == nullptr) return fail(FL_ERR_INVALID, "null decode parameters");
+  return decode_call(p, p->workspace, p->workspace_bytes, stream);
+}
+
+int fl_decode_noalloc(const fl_decode_params* p, fl_stream_t stream) {
   if (int rc = check_decode_shape(p)) return rc;
-  if (!p->q || !p->k_cache || !p->v_cache || !p->o || !p->lse || !p->seq_lens)
-    return fail(FL_ERR_INVALID, "null tensor pointer");
-  if (!valid_scale(p->softmax_scale)) return fail(FL_ERR_INVALID, "softmax_scale must be positive");
-  if (p->num_splits < 1 || p->num_splits > fl::kMaxSplits)
-    return fail(FL_ERR_INVALID, "num_splits must be in [1, 128]");
-  const int eb = elem_bytes(p->dtype);
-  if (!rows_16_byte(p->q, eb, p->batch, p->q_batch_stride, p->heads, p->q_head_stride, 1, 0))
-    return fail(FL_ERR_INVALID, "q must have 16-byte aligned rows");
-  // Cache dimensions: [B, S_max] rows, or [num_blocks, page_size] for a paged cache.
-  const int64_t outer = p->block_tables != nullptr ? p->num_blocks : p->batch;
-  const int64_t rows = p->block_tables != nullptr ? p->page_size : p->max_seqlen;
-  if (!rows_16_byte(p->k_cache, eb, outer, p->k_batch_stride, rows, p->k_seq_stride, p->heads_kv,
-                    p->k_head_stride))
-    return fail(FL_ERR_INVALID, "k_cache must have 16-byte aligned rows (data pointer and strides)");
-  if (!rows_16_byte(p->v_cache, eb, outer, p->v_batch_stride, rows, p->v_seq_stride, p->heads_kv,
-                    p->v_head_stride))
-    return fail(FL_ERR_INVALID, "v_cache must have 16-byte aligned rows (data pointer and strides)");
-  if (!aligned(p->o, eb) || !aligned(p->lse, 4) || !aligned(p->seq_lens, 4))
-    return fail(FL_ERR_INVALID, "o, lse and seq_lens must be aligned to their element size");
-  if (p->block_tables != nullptr && !aligned(p->block_tables, 4))
-    return fail(FL_ERR_INVALID, "block_tables must be 4-byte aligned");
-
-  const int group = p->heads / p->heads_kv;
-  const fl::DType dt = decode_dtype(p->dtype);
-  const fl::DecodeLayout layout = fl::decode_layout(dt, p->head_dim, p->heads_kv, group);
-  const int head_chunks = group / layout.heads_per_wg;
-  const int64_t blocks = static_cast<int64_t>(p->batch) * p->heads_kv * head_chunks * p->num_splits;
-  if (blocks > (int64_t{1} << 24) || static_cast<int64_t>(p->batch) * p->heads > (int64_t{1} << 24))
-    return fail(FL_ERR_INVALID, "batch * heads too large");
-
-  fl::DecodeArgs a{};
-  a.q = p->q;
-  a.k = p->k_cache;
-  a.v = p->v_cache;
-  a.o = p->o;
-  a.lse = p->lse;
-  a.seq_lens = p->seq_lens;
-  a.q_bs = p->q_batch_stride;
-  a.q_hs = p->q_head_stride;
-  a.k_bs = p->k_batch_stride;
-  a.k_ss = p->k_seq_stride;
-  a.k_hs = p->k_head_stride;
-  a.v_bs = p->v_batch_stride;
-  a.v_ss = p->v_seq_stride;
-  a.v_hs = p->v_head_stride;
-  a.o_bs = p->o_batch_stride;
-  a.o_hs = p->o_head_stride;
-  a.batch = p->batch;
-  a.heads = p->heads;
-  a.heads_kv = p->heads_kv;
-  a.group = group;
-  a.max_seqlen = p->max_seqlen;
-  a.num_splits = p->num_splits;
-  a.head_chunks = head_chunks;
-  a.kv_span = decode_span(p, layout, p->num_splits);
-  a.mfma = layout.mfma;
-  a.block_tables = p->block_tables;
-  a.block_tables_stride = p->block_tables_stride;
-  a.page_size = p->page_size;
-  a.num_blocks = p->num_blocks;
-  a.page_table_global =
-      p->block_tables != nullptr &&
-      pages_per_split(p->max_seqlen, p->num_splits, p->page_size) > fl::kMaxSplitPages;
-  if (a.page_table_global) a.kv_span = 1;
-  a.page_shift = -1;
-  for (int s = 0; s < 31; ++s)
-    if (p->page_size == (1 << s)) a.page_shift = s;
-  a.scale_log2 = static_cast<float>(p->softmax_scale * 1.4426950408889634);
+  float* ws = nullptr;
   if (p->num_splits > 1) {
-    const size_t need =
-        static_cast<size_t>(p->batch) * p->heads * p->num_splits * (p->head_dim + 2) * sizeof(float);
-    if (p->workspace == nullptr || p->workspace_bytes < need)
-      return fail(FL_ERR_INVALID, "decode workspace is missing or smaller than fl_decode_plan reports");
-    if (!aligned(p->workspace, 16)) return fail(FL_ERR_INVALID, "decode workspace must be 16-byte aligned");
-    a.partial_o = p->workspace;
-    a.partial_ml =
-        p->workspace + static_cast<size_t>(p->batch) * p->heads * p->num_splits * p->head_dim;
+    // Compared in floating point so that no product of the sizes can overflow before the check.
+    const double need = static_cast<double>(p->batch) * p->heads * p->num_splits *
+                        (p->head_dim + 2) * sizeof(float);
+    if (need > static_cast<double>(kScratchBytes))
+      return fail(FL_ERR_INVALID,
+                  fmt("fl_decode_noalloc: the split workspace (%lld bytes) exceeds the library's "
+                      "16 MiB scratch array; use fewer splits or fl_decode",
+                      static_cast<long long>(need)));
+    if (int rc = scratch_for_current_device(&ws)) return rc;
   }
-  const hipError_t err = fl::launch_decode(a, dt, p->head_dim, static_cast<hipStream_t>(stream));
-  if (err != hipSuccess) return fail(FL_ERR_LAUNCH, std::string("decode launch: ") + hipGetErrorString(err));
-  return FL_OK;
+  return decode_call(p, ws, kScratchBytes, stream);
 }
 
 int fl_smoke_axpy(const float* x, const float* y, float alpha, float* out, int64_t n,

@@ -114,6 +114,7 @@ SIGNATURES = {
         ],
     ),
     "fl_decode": (ctypes.c_int, [ctypes.POINTER(DecodeParams), ctypes.c_void_p]),
+    "fl_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(DecodeParams), ctypes.c_void_p]),
     "fl_smoke_axpy": (
         ctypes.c_int,
         [
@@ -385,6 +386,23 @@ def decode(q, k_cache, v_cache, seq_lens, softmax_scale: float, num_splits: int,
     with _on_device(q.device):
         _check(LIB.fl_decode(ctypes.byref(p), _stream(q.device)))
     return o, lse
+
+
+def decode_noalloc(q, k_cache, v_cache, seq_lens, o, lse, softmax_scale: float, num_splits: int,
+                   block_tables=None) -> int:
+    """fl_decode_noalloc on caller-provided outputs o [B, H, D] and lse [B, H]: the split workspace
+    is the library's own scratch array, so nothing is allocated. num_splits 0 takes the planned
+    count. Returns the split count used. The arguments are taken as valid (the public ops check
+    them); this is the allocation-free path for callers that manage their own buffers."""
+    p = _decode_params(q, k_cache, v_cache, seq_lens, o, lse, softmax_scale, block_tables)
+    index = q.device.index if q.device.index is not None else torch.cuda.current_device()
+    splits, ws_bytes = ctypes.c_int32(), ctypes.c_size_t()
+    _check(LIB.fl_decode_plan(ctypes.byref(p), int(num_splits), 1, cu_count(index),
+                              ctypes.byref(splits), ctypes.byref(ws_bytes)))
+    p.num_splits = splits.value
+    with _on_device(q.device):
+        _check(LIB.fl_decode_noalloc(ctypes.byref(p), _stream(q.device)))
+    return splits.value
 
 
 def decode_plan(batch, heads, heads_kv, head_dim, max_seqlen, dtype, num_splits=0,

@@ -130,6 +130,26 @@ int fl_decode_plan(const fl_decode_params* p, int32_t requested_splits, int32_t 
  */
 int fl_decode(const fl_decode_params* p, fl_stream_t stream);
 
+/*
+ * fl_decode without a caller workspace: the split partials go to a scratch
+ * array the library holds in device memory (a file-scope __device__ array of
+ * 16 MiB; each GPU the library runs on holds its own copy until the process
+ * ends). No counterpart in the reference: this entry point is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). It allocates nothing
+ * itself: no hipMalloc, no hipFree, no allocating library call.
+ *
+ * Parameters are fl_decode's; workspace and workspace_bytes are ignored. The
+ * kernels run on `stream`, which must belong to the current device. A call
+ * whose workspace (B * H * num_splits * (head_dim + 2) * 4 bytes, 0 for one
+ * split) exceeds 16 MiB is rejected with FL_ERR_INVALID before any launch.
+ * Every call on a GPU shares that GPU's array: calls on one stream are
+ * ordered and safe, calls that overlap on one GPU (several streams or
+ * threads at once) race. The kernels write every partial they read, so the
+ * array's previous contents never reach an output.
+ */
+int fl_decode_noalloc(const fl_decode_params* p, fl_stream_t stream);
+
 /* out = alpha * x + y over n fp32 elements (reference csrc/common/smoke.cu:12-45). */
 int fl_smoke_axpy(const float* x, const float* y, float alpha, float* out, int64_t n,
                   fl_stream_t stream);

@@ -244,3 +244,16 @@ def test_paged_decode_rejects_bad_geometry():
 def test_tile_test_rejects_bad_k():
     assert _hip.LIB.fl_mfma_tile_test(256, 256, 256, 48, 0, None) != 0
     assert "K in {16, 32, 64}" in _hip.LIB.fl_last_error().decode()
+
+
+def test_noalloc_decode_rejects_workspaces_beyond_its_scratch_array():
+    # fl_decode_noalloc keeps the split partials in a 16 MiB array of its own; a call that would
+    # need more is refused on the host, before any device call (so this runs without a GPU).
+    p = _hip.DecodeParams()
+    p.batch, p.heads, p.heads_kv, p.head_dim, p.max_seqlen = 64, 64, 8, 128, 32768
+    p.num_splits, p.dtype, p.softmax_scale = 128, 0, 0.088
+    assert _hip.LIB.fl_decode_noalloc(ctypes.byref(p), None) == 1
+    assert b"exceeds the library's 16 MiB scratch array" in _hip.LIB.fl_last_error()
+    p.heads_kv = 7  # shape errors come first, as in fl_decode
+    assert _hip.LIB.fl_decode_noalloc(ctypes.byref(p), None) == 1
+    assert b"multiple of KV heads" in _hip.LIB.fl_last_error()
