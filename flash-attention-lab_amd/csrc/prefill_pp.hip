@@ -67,9 +67,11 @@ static_assert(kStages == 3 || kStages == 4, "3 or 4 ring stages");
 #ifndef FL_PP_SETPRIO
 #define FL_PP_SETPRIO 1
 #endif
-// MFMAs whose A-operand fragments are in flight ahead of the one issuing.
+// MFMAs whose A-operand fragments are in flight ahead of the one issuing. Two keep the MFMA phase
+// as fast as four did and leave the registers that the peeled first and last periods need (with
+// four, the kernel spilled at head_dim 128).
 #ifndef FL_PP_AHEAD
-#define FL_PP_AHEAD 4
+#define FL_PP_AHEAD 2
 #endif
 
 __device__ __forceinline__ float max_of(const f32x16& x, const f32x16& y) {
@@ -120,9 +122,11 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   constexpr int kSlotBytes = 2 * kTile;
   constexpr int kVRingBytes = kStages * kSlotBytes;
   static_assert(kVRingBytes <= 65536, "K ring must fit the immediate range");
-  auto k_slot = [&](auto s) -> uint16_t* { return smem + (decltype(s)::value % kStages) * kTile; };
+  // Ring slots are ints: compile-time constants in the unrolled tile loop (folded into the LDS
+  // instructions' immediates), run-time values only in a block's last period.
+  auto k_slot = [&](int s) -> uint16_t* { return smem + (static_cast<unsigned>(s) % kStages) * kTile; };
   // Byte offset of V slot s from the biased per-lane V offsets.
-  auto v_slot_offset = [&](auto s) constexpr { return (decltype(s)::value % kStages) * kSlotBytes; };
+  auto v_slot_offset = [&](int s) { return (static_cast<unsigned>(s) % kStages) * kSlotBytes; };
   const char* lds_bytes = reinterpret_cast<const char*>(smem);
 
   const int tid = threadIdx.x;
@@ -225,14 +229,14 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
       return buffer_words(p, bytes);
     };
     // Block j of the group's tile (descriptor `w`) into ring slot kSlot.
-    auto issue_block = [&](u32x4s w, auto slot_tag, auto j_tag) {
+    auto issue_block = [&](u32x4s w, int slot, auto j_tag) {
       constexpr int j = decltype(j_tag)::value;
-      constexpr uint32_t kOff = (decltype(slot_tag)::value % kStages) * kSlotBytes + j * 1024;
-      buffer_load16_to_lds_asm(w, lds_wave + kOff, my_off[j]);
+      const uint32_t off = (static_cast<unsigned>(slot) % kStages) * kSlotBytes + j * 1024;
+      buffer_load16_to_lds_asm(w, lds_wave + off, my_off[j]);
     };
-    auto load_tile = [&](int t, auto slot_tag) {
+    auto load_tile = [&](int t, int slot) {
       const u32x4s w = tile_words(t);
-      static_for<0, kDmaPerWave>([&](auto j) { issue_block(w, slot_tag, j); });
+      static_for<0, kDmaPerWave>([&](auto j) { issue_block(w, slot, j); });
     };
 
     f32x16 o[D / 32];
@@ -261,24 +265,38 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     constexpr int kAhead = FL_PP_AHEAD;
     static_assert(kAhead >= 1 && kAhead <= kPv, "prefetched fragments are V fragments");
     static_assert(8 * (kDmaPerWave - 1) + 1 < kSteps, "one tile load every 8 MFMAs");
-    auto read_frag = [&](auto slot_tag, auto i_tag) -> u32x4 {
-      constexpr int kS = decltype(slot_tag)::value;
+    // Fragment of MFMA i of the phase with slots kS = m % kStages: V(m - 1) sits in V slot
+    // kS + kStages - 1, K(m) in K slot kS.
+    auto read_frag = [&](int slot, auto i_tag) -> u32x4 {
       constexpr int i = decltype(i_tag)::value;
       if constexpr (i < kPv) {
         constexpr int kk = i / (D / 32), nb = i % (D / 32);
-        const char* vt = lds_bytes + v_slot_offset(std::integral_constant<int, kS + kStages - 1>{});
+        const char* vt = lds_bytes + v_slot_offset(slot + kStages - 1);
         return v_frag_at(vt + kk * kKeyStepBytes<D>, v_lds[nb][0], v_lds[nb][1]);
       } else {
         constexpr int j = i - kPv, ks = j / 2, blk = j % 2;
-        const char* kt = reinterpret_cast<const char*>(k_slot(std::integral_constant<int, kS>{}));
+        const char* kt = reinterpret_cast<const char*>(k_slot(slot));
         return lds_load16(kt + blk * kKeyBlockBytes<D>, k_lds[ks]);
       }
     };
-    u32x4 fr[kSteps];
-    auto prefetch = [&](auto slot_tag) {
-      static_for<0, kAhead>([&](auto i) { fr[decltype(i)::value] = read_frag(slot_tag, i); });
+    // The first kAhead fragments of the next MFMA phase (P V's, or K Q^T's for a phase with K Q^T
+    // only), read at the end of the wave's softmax phase. Only these cross from one phase to the
+    // next: the rest of a phase's fragments live in that phase.
+    u32x4 pre[kAhead];
+    auto prefetch = [&](int slot) {
+      static_for<0, kAhead>([&](auto i) { pre[decltype(i)::value] = read_frag(slot, i); });
     };
-    auto mfma_phase = [&](auto slot_tag, auto&& hook) {
+    auto prefetch_qk = [&](int slot) {
+      static_for<0, kAhead>([&](auto i) {
+        pre[decltype(i)::value] = read_frag(slot, std::integral_constant<int, kPv + decltype(i)::value>{});
+      });
+    };
+    auto mfma_phase = [&](int slot, auto pv_tag, auto qk_tag, auto&& hook) {
+      constexpr bool kDoPv = decltype(pv_tag)::value;
+      constexpr bool kDoQk = decltype(qk_tag)::value;
+      constexpr int kFirstStep = kDoPv ? 0 : kPv;
+      u32x4 fr[kSteps];
+      static_for<0, kAhead>([&](auto i) { fr[kFirstStep + decltype(i)::value] = pre[decltype(i)::value]; });
       auto issue = [&](auto i_tag, const u32x4& f) {
         constexpr int i = decltype(i_tag)::value;
         if constexpr (i < kPv) {
@@ -296,9 +314,11 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
       __builtin_amdgcn_sched_barrier(0);
       static_for<0, kSteps>([&](auto i) {
         constexpr int n = decltype(i)::value;
-        issue(i, fr[n]);
-        if constexpr (n + kAhead < kSteps) {
-          fr[n + kAhead] = read_frag(slot_tag, std::integral_constant<int, n + kAhead>{});
+        constexpr bool kLive = n < kPv ? kDoPv : kDoQk;
+        if constexpr (kLive) issue(i, fr[n]);
+        // Read ahead only the fragments of live steps (a K Q^T-only phase has them prefetched).
+        if constexpr (n + kAhead < kSteps && (n + kAhead < kPv ? kDoPv : (kDoQk && (kDoPv || n >= kPv)))) {
+          fr[n + kAhead] = read_frag(slot, std::integral_constant<int, n + kAhead>{});
         }
         hook(i);
         __builtin_amdgcn_sched_barrier(0);
@@ -306,6 +326,11 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
 #if FL_PP_SETPRIO == 1
       __builtin_amdgcn_s_setprio(0);
 #endif
+    };
+    // A phase whose MFMAs nobody in the group needs (causal tiles past the diagonal of all of the
+    // group's rows): only its tile loads.
+    auto loads_only = [&](auto&& hook) {
+      static_for<0, kSteps>([&](auto i) { hook(i); });
     };
 
     // P(t) from S(t) against the reference point: p = 2^(s scale_log2 + neg_shift), packed (rounded
@@ -393,9 +418,9 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     static_for<0, kStages - 1>([&](auto i_tag) {
       constexpr int i = decltype(i_tag)::value;
       if (group == 0) {
-        load_tile(i, i_tag);
+        load_tile(i, i);
       } else {
-        load_tile(i - 1, std::integral_constant<int, i + kStages - 1>{});
+        load_tile(i - 1, i + kStages - 1);
       }
     });
     wait_vmcnt<(kStages - 2) * kDmaPerWave>();
@@ -403,92 +428,140 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
 
     // Period m: half-period 2m then 2m + 1. Group 0: MFMA(m), softmax(m). Group 1: softmax(m - 1),
     // then MFMA(m). Each MFMA phase issues its group's next tile between its MFMAs (the descriptor
-    // after MFMA 0, block j after MFMA 8j + 1). Each group runs its own straight-line loop, unrolled
-    // by kStages so that ring slots are compile-time immediates; the periods % kStages left over run
-    // after it.
-    const int periods = num_tiles + 1;  // the last one only finishes P V of the last tile
+    // after MFMA 0, block j after MFMA 8j + 1). A group's periods run in four kinds:
+    //  * first (m = 0): K Q^T only, as there is no tile -1 for a P V;
+    //  * full, m = 1 .. G - 1, as a straight-line loop unrolled by kStages from slot 1 so that ring
+    //    slots are compile-time immediates;
+    //  * last (m = G): P V of tile G - 1 only, its slot G % kStages a run-time value;
+    //  * loads only, m = G + 1 .. num_tiles: the group's tile loads and waits (the other group may
+    //    still read those tiles) but no MFMAs,
+    // where G is the number of tiles any row of the group sees: num_tiles, or fewer for the group of
+    // earlier rows on a causal diagonal, whose tiles past those rows' diagonal it skips. Both groups
+    // run num_tiles + 1 periods of two barriers each.
+    int group_tiles = num_tiles;
+    if (a.causal) {
+      const int last = q0 + (group + 1) * kLoadWaves * kRowsPerWave - 1 + a.causal_offset;
+      group_tiles = last < 0 ? 0 : min(num_tiles, last / kBlockN + 1);
+    }
+    using kFirstT = std::integral_constant<int, 0>;
+    using kFullT = std::integral_constant<int, 1>;
+    using kLastT = std::integral_constant<int, 2>;
+    using kLoadsT = std::integral_constant<int, 3>;
     auto run = [&](auto group_tag) {
       constexpr int kGroup = decltype(group_tag)::value;
-      auto period = [&](int m, auto slot_tag) {
-        constexpr int kS = decltype(slot_tag)::value;
+      // Group 0 loads K(m + kStages - 1) into slot (m - 1) % kStages, group 1 V(m + kStages - 2)
+      // into slot (m - 2) % kStages.
+      constexpr int kLead = kGroup == 0 ? kStages - 1 : kStages - 2;
+      auto period = [&](int m, int slot, auto mode_tag) {
+        constexpr int kMode = decltype(mode_tag)::value;
+        constexpr bool kDoPv = kMode == kFullT::value || kMode == kLastT::value;
+        constexpr bool kDoQk = kMode == kFirstT::value || kMode == kFullT::value;
+        u32x4s w;
+        auto hook = [&](auto i_tag) {
+          constexpr int i = decltype(i_tag)::value;
+          if constexpr (i == 0) w = tile_words(m + kLead);
+          if constexpr (i % 8 == 1 && i / 8 < kDmaPerWave) {
+            issue_block(w, slot + kLead, std::integral_constant<int, i / 8>{});
+          }
+        };
+        auto mfma = [&]() {
+          if constexpr (kMode == kLoadsT::value) {
+            loads_only(hook);
+          } else {
+            mfma_phase(slot, std::bool_constant<kDoPv>{}, std::bool_constant<kDoQk>{}, hook);
+          }
+        };
         if constexpr (kGroup == 0) {
-          if (m == 0) prefetch(slot_tag);
-          // K(m + kStages - 1) into slot (m - 1) % kStages.
-          u32x4s w;
-          mfma_phase(slot_tag, [&](auto i_tag) {
-            constexpr int i = decltype(i_tag)::value;
-            if constexpr (i == 0) w = tile_words(m + kStages - 1);
-            if constexpr (i % 8 == 1 && i / 8 < kDmaPerWave) {
-              issue_block(w, std::integral_constant<int, kS + kStages - 1>{},
-                          std::integral_constant<int, i / 8>{});
-            }
-          });
+          if constexpr (kMode == kFirstT::value) prefetch_qk(slot);
+          mfma();
           phase_barrier();
-          // The next MFMA phase's first fragments (V(m), published by the barrier that ended
-          // half-period 2m), read first so their latency hides behind the softmax.
-          prefetch(std::integral_constant<int, kS + 1>{});
-          softmax_phase(m);
+          if constexpr (kDoQk) {
+            // The next MFMA phase's first fragments (V(m), published by the barrier that ended
+            // half-period 2m), read first so their latency hides behind the softmax.
+            prefetch(slot + 1);
+            softmax_phase(m);
+          }
           wait_vmcnt<kPendingK>();  // K(m + 1), first read in half-period 2m + 2
           phase_barrier();
         } else {
-          prefetch(slot_tag);
-          softmax_phase(m - 1);
+          if constexpr (kMode == kFirstT::value) prefetch_qk(slot);
+          if constexpr (kDoPv) {
+            prefetch(slot);
+            softmax_phase(m - 1);
+          }
           wait_vmcnt<kPendingV>();  // V(m), first read in half-period 2m + 1
           phase_barrier();
-          // V(m + kStages - 2) into slot (m - 2) % kStages.
-          u32x4s w;
-          mfma_phase(slot_tag, [&](auto i_tag) {
-            constexpr int i = decltype(i_tag)::value;
-            if constexpr (i == 0) w = tile_words(m + kStages - 2);
-            if constexpr (i % 8 == 1 && i / 8 < kDmaPerWave) {
-              issue_block(w, std::integral_constant<int, kS + kStages - 2>{},
-                          std::integral_constant<int, i / 8>{});
-            }
-          });
+          mfma();
           phase_barrier();
         }
       };
+      if (num_tiles == 0) return;  // no key at all: nothing to multiply
       int m = 0;
-      for (; m + kStages <= periods; m += kStages) {
-        period(m, std::integral_constant<int, 0>{});
-        period(m + 1, std::integral_constant<int, 1>{});
-        period(m + 2, std::integral_constant<int, 2>{});
-        if constexpr (kStages > 3) period(m + 3, std::integral_constant<int, 3>{});
+      if (group_tiles > 0) {
+        period(0, 0, kFirstT{});
+        for (m = 1; m < group_tiles;) {
+          bool done = false;
+          static_for<0, kStages>([&](auto j) {
+            if (done) return;
+            period(m, (1 + decltype(j)::value) % kStages, kFullT{});
+            done = ++m == group_tiles;
+          });
+        }
+        period(m, m % kStages, kLastT{});
+        ++m;
       }
-      const int rest = periods - m;
-      if (rest > 0) period(m, std::integral_constant<int, 0>{});
-      if (rest > 1) period(m + 1, std::integral_constant<int, 1>{});
-      if constexpr (kStages > 3) {
-        if (rest > 2) period(m + 2, std::integral_constant<int, 2>{});
-      }
+      for (; m <= num_tiles; ++m) period(m, m % kStages, kLoadsT{});
     };
     if (group == 0) {
       run(std::integral_constant<int, 0>{});
     } else {
       run(std::integral_constant<int, 1>{});
     }
-    // Loads past the end may still be in flight into free slots; they must land before the
-    // workgroup's LDS is handed to another workgroup.
+    // Loads past the end may still be in flight into free slots: each wave waits for its own here,
+    // and the barrier below for the others', before the ring is reused.
     wait_vmcnt<0>();
 
     const float lt = sum_halves(l);
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    if (my_row < a.seqlen_q) {
-      uint16_t* orow = a.o + b * a.o_bs + static_cast<int64_t>(my_row) * a.o_ss + h * a.o_hs;
+    // Output rows go back whole, 16 bytes per lane (the accumulator layout would store 8 bytes per
+    // lane into 32 rows a row stride apart): each wave stages its 32 rows in its own part of the
+    // ring, rows padded by 16 bytes so that the row-per-lane writes spread over the banks, then
+    // stores kRowsPerStore whole rows per instruction. Every staging address is one per-lane base
+    // plus an immediate, so the addresses hold two registers (the bases are invariant across the
+    // blocks of a causal workgroup and would otherwise stay live through the tile loop).
+    phase_barrier();
+    constexpr int kChunks = D / 8;
+    constexpr int kStageRow = 2 * D + 16;
+    constexpr int kRowsPerStore = 64 / kChunks;
+    static_assert(kPpWaves * kRowsPerWave * kStageRow <= static_cast<int>(sizeof(smem)), "staging fits");
+    char* stage = reinterpret_cast<char*>(smem) + wave * kRowsPerWave * kStageRow;
+    {
+      char* wbase = stage + (lane & 31) * kStageRow + 8 * half;
 #pragma unroll
       for (int nb = 0; nb < D / 32; ++nb) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int d = 32 * nb + 8 * g + 4 * half;
+          // Dims 32 nb + 8 g + 4 half .. + 3: half of 16-byte chunk 4 nb + g of this lane's row.
           const u32x2 packed{E::pack2(o[nb][4 * g] * inv, o[nb][4 * g + 1] * inv),
                              E::pack2(o[nb][4 * g + 2] * inv, o[nb][4 * g + 3] * inv)};
-          *reinterpret_cast<u32x2*>(orow + d) = packed;
+          *reinterpret_cast<u32x2*>(wbase + 16 * (4 * nb + g)) = packed;
         }
       }
-      if (half == 0) {
-        a.lse[(static_cast<int64_t>(b) * a.heads + h) * a.seqlen_q + my_row] =
-            lt > 0.f ? ref * kLn2 + logf(lt) : -INFINITY;
+    }
+    {
+      const int chunk = lane % kChunks;
+      const char* rbase = stage + (lane / kChunks) * kStageRow + 16 * chunk;
+      uint16_t* obase = a.o + b * a.o_bs + h * a.o_hs + 8 * chunk;
+#pragma unroll
+      for (int j = 0; j < kRowsPerWave / kRowsPerStore; ++j) {
+        const int r = row0 + j * kRowsPerStore + lane / kChunks;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(rbase + j * kRowsPerStore * kStageRow);
+        if (r < a.seqlen_q) *reinterpret_cast<u32x4*>(obase + static_cast<int64_t>(r) * a.o_ss) = v;
       }
+    }
+    if (my_row < a.seqlen_q && half == 0) {
+      a.lse[(static_cast<int64_t>(b) * a.heads + h) * a.seqlen_q + my_row] =
+          lt > 0.f ? ref * kLn2 + logf(lt) : -INFINITY;
     }
   };
 
@@ -496,7 +569,9 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   const int heavy = a.q_blocks - 1 - item;
   const int blocks_here = a.causal && item < heavy ? 2 : 1;
   for (int i = 0; i < blocks_here; ++i) {
-    if (i > 0) __syncthreads();  // the next block's prologue refills slots other waves just read
+    // The next block's prologue refills the ring, which the epilogue's staging reads just used (no
+    // memory fence: the output stores need not complete first).
+    if (i > 0) phase_barrier();
     process(!a.causal ? item : i == 0 ? heavy : item);
   }
 }
