@@ -374,13 +374,20 @@ decode_split_kernel(const DecodeArgs a) {
       l[g] = lsum;
     }
   };
+  // The prefetches are unconditional (past the end they re-read the split's last row, which the
+  // cache serves), and a scheduling barrier keeps them ahead of the current batch's use. Without
+  // either, the compiler waits for every load in flight, the prefetch included, before it uses the
+  // current batch, or moves the K loads down to their dot products: one batch in flight instead of
+  // two (B1-MHA 89.2 -> 88.5 us, B=1 with 8 KV heads on this kernel 41.8 -> 38.3 us).
   u32x4 ka[kUnroll], va[kUnroll], kb[kUnroll], vb[kUnroll];
   if (k_begin < k_end) load_batch(k_begin, ka, va);
   for (int base = k_begin; base < k_end; base += 2 * kKeysPerIter) {
-    if (base + kKeysPerIter < k_end) load_batch(base + kKeysPerIter, kb, vb);
+    load_batch(base + kKeysPerIter, kb, vb);
+    __builtin_amdgcn_sched_barrier(0);
     use_batch(base, ka, va);
     if (base + kKeysPerIter >= k_end) break;
-    if (base + 2 * kKeysPerIter < k_end) load_batch(base + 2 * kKeysPerIter, ka, va);
+    load_batch(base + 2 * kKeysPerIter, ka, va);
+    __builtin_amdgcn_sched_barrier(0);
     use_batch(base + kKeysPerIter, kb, vb);
   }
 

@@ -201,7 +201,10 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
 #pragma unroll
       for (int nb = 0; nb < D / 32; ++nb) vf[kk][nb] = v_frag<D>(vt, nb, kk, lane);
     }
-    if (i + kAhead < my_tiles) load_tile(i + kAhead, r);
+    // Unconditional (past the split the keys clamp to its last row): a load skipped on some path
+    // leaves the compiler unsure how many are in flight, and it then waits for all of them.
+    load_tile(i + kAhead, r);
+    __builtin_amdgcn_sched_barrier(0);
 
     f32x16 s = f32x16{};
 #pragma unroll
@@ -241,11 +244,19 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
     }
   };
 
-  Regs r[kAhead];
-  static_for<0, kAhead>([&](auto t) __attribute__((always_inline)) {
-    if (decltype(t)::value < my_tiles) load_tile(decltype(t)::value, r[decltype(t)::value]);
-  });
-  for (int i = 0; i < my_tiles; i += kAhead) {
+  // Guarded as a whole so the first loads are unconditional too (a split with no tile for this
+  // wave has no valid row to clamp to).
+  if (my_tiles > 0) {
+    Regs r[kAhead];
+    static_for<0, kAhead>([&](auto t) __attribute__((always_inline)) {
+      load_tile(decltype(t)::value, r[decltype(t)::value]);
+    });
+    int i = 0;
+    for (; i + kAhead <= my_tiles; i += kAhead) {
+      static_for<0, kAhead>([&](auto t) __attribute__((always_inline)) {
+        step(i + decltype(t)::value, r[decltype(t)::value]);
+      });
+    }
     static_for<0, kAhead>([&](auto t) __attribute__((always_inline)) {
       if (i + decltype(t)::value < my_tiles) step(i + decltype(t)::value, r[decltype(t)::value]);
     });
