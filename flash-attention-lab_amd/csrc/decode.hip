@@ -19,7 +19,7 @@
 //  * Each lane has kUnroll rows of K and of V in flight in each of two register buffers
 //    (non-temporal loads: the cache is read once). The rows stay packed: q.k goes through v_dot2
 //    (bf16, fp16) and V elements are unpacked one at a time where they are used, which keeps the
-//    kernel at 96 registers for one query head (five workgroups per CU) and 168 up to four.
+//    kernel at 63 registers for one query head and 161 for four.
 //  * At the end the row groups are merged by a fixed butterfly inside each wave, then the four
 //    waves in order through LDS. With one split the workgroup writes o and lse; otherwise it
 //    writes its unnormalized partial output and (max, sum), and decode_merge_kernel combines the
@@ -39,9 +39,12 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 // Cache rows of K and of V per lane in each of the two register buffers, for workgroups serving
 // fewer than four query heads (FL_DECODE_UNROLL) and four or more (FL_DECODE_UNROLL_GQA, whose
-// per-head state takes more registers).
+// per-head state takes more registers). With the prefetch kept in flight (the scheduling barrier
+// in the key loop), two rows stream fastest for one query head: B1-MHA 87.7 -> 83.2-83.7 us,
+// B8-MHA 645 -> 641-643 us against four rows; one row 110 us, three 89.7 us. Four query heads
+// and more keep four rows (two: B8 with 8 per KV head 232 -> 258 us).
 #ifndef FL_DECODE_UNROLL
-#define FL_DECODE_UNROLL 4
+#define FL_DECODE_UNROLL 2
 #endif
 #ifndef FL_DECODE_UNROLL_GQA
 #define FL_DECODE_UNROLL_GQA 4
