@@ -20,16 +20,19 @@
 //  * Workgroup: 8 waves x 32 query rows = 256 rows of one (batch, head). Waves w and w + 4 share a
 //    SIMD (the dispatcher deals waves to SIMDs with period 4). Group 0 is waves 0-3, group 1 waves
 //    4-7: one wave of each group per SIMD.
-//  * Time is cut into half-periods by workgroup barriers. In half-period 2m group 0 runs
-//    MFMA(m) = P V of tile m-1 then S = K Q^T of tile m (32 MFMAs) while group 1 runs the softmax
-//    of tile m-1; in half-period 2m+1 the roles swap.
+//  * Time is cut into periods by workgroup barriers, one per tile. In the first half of period m
+//    group 0 runs MFMA(m) = P V of tile m-1 then S = K Q^T of tile m (32 MFMAs) while group 1 runs
+//    the softmax of tile m-1; in the second half the roles swap. Nothing holds the groups to the
+//    half-period boundary: they keep the offset by themselves (contention for the MFMA pipe), and a
+//    barrier in the middle of each period measured 1-1.6% slower.
 //  * K and V tiles (64 keys) stream through a ring of kStages LDS slots each, filled by direct
 //    global -> LDS loads (buffer_load ... lds) issued between the MFMAs of the MFMA phases: group 0
-//    loads K(m + kStages - 1) in half-period 2m, group 1 V(m + kStages - 2) in half-period 2m+1
+//    loads K(m + kStages - 1) in the first half of period m, group 1 V(m + kStages - 2) in the second
 //    (4 loads per wave each at D = 128, 2 at D = 64; a load costs the issuing wave about 70
-//    cycles, which the MFMA phase has to spare). Each group waits for its own tiles at the end of its softmax phase just before
-//    they are first read. Loads past the last tile use an empty buffer resource (they write zeros
-//    into a free slot) so every wave issues the same number of loads and the vmcnt accounting is
+//    cycles, which the MFMA phase has to spare). Each group waits for its own tiles at the end of a
+//    period, so the barrier that ends it publishes them before their first read. Loads past the
+//    last tile use an empty buffer resource (they write zeros into a free slot) so every wave
+//    issues the same number of loads and the vmcnt accounting is
 //    uniform.
 //  * Work order: XCD-contiguous (batch, head) ranges (workgroups are dealt round-robin over the 8
 //    XCDs, each with its own L2); causal query blocks in heavy/light pairs per workgroup.
@@ -56,8 +59,8 @@ constexpr float kSumLimit = 32768.f;
 // still give 0, with no separate test for "no reference yet".
 constexpr float kNoRef = -1e30f;
 
-// LDS ring depth (K and V slots each). A tile is issued 2 kStages - 4 (K) or 2 kStages - 5 (V)
-// half-periods before the half-period that first reads it.
+// LDS ring depth (K and V slots each). A K tile is issued kStages - 1 periods before the period
+// that first reads it, a V tile kStages - 2 (in the second half of its period).
 #ifndef FL_PP_STAGES
 #define FL_PP_STAGES 4
 #endif
@@ -407,14 +410,16 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
 #endif
     };
 
-    // Each group waits for its own loads at the end of its softmax phase in period m: group 0 for
-    // K(m + 1) (first read in half-period 2m + 2) with the kStages - 2 later K tiles still in flight,
-    // group 1 for V(m) (first read in half-period 2m + 1) with the kStages - 3 later V tiles.
+    // Each group waits for its own loads at the end of period m: group 0 for K(m + 1) (first read
+    // in period m + 1) with the kStages - 2 later K tiles still in flight, group 1 for V(m + 1)
+    // (first read in period m + 1, by group 0's fragment prefetch) with the kStages - 3 later V
+    // tiles.
     constexpr int kPendingK = (kStages - 2) * kDmaPerWave;
     constexpr int kPendingV = (kStages - 3) * kDmaPerWave;
 
-    // Prologue: group 0 loads K(0 .. kStages - 2), group 1 V(-1 .. kStages - 3) (V(-1) is zeros, the
-    // P V of period 0); K(0) and V(-1) must be in LDS before the first half-period.
+    // Prologue: group 0 loads K(0 .. kStages - 2), group 1 V(-1 .. kStages - 3) (V(-1) stands for
+    // the P V that period 0 does not run, so every wave issues the same loads); K(0) and V(0) must
+    // be in LDS before period 0.
     static_for<0, kStages - 1>([&](auto i_tag) {
       constexpr int i = decltype(i_tag)::value;
       if (group == 0) {
@@ -423,10 +428,14 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
         load_tile(i - 1, i + kStages - 1);
       }
     });
-    wait_vmcnt<(kStages - 2) * kDmaPerWave>();
+    if (group == 0) {
+      wait_vmcnt<(kStages - 2) * kDmaPerWave>();
+    } else {
+      wait_vmcnt<(kStages - 3) * kDmaPerWave>();
+    }
     phase_barrier();
 
-    // Period m: half-period 2m then 2m + 1. Group 0: MFMA(m), softmax(m). Group 1: softmax(m - 1),
+    // Period m, one barrier at its end. Group 0: MFMA(m), softmax(m). Group 1: softmax(m - 1),
     // then MFMA(m). Each MFMA phase issues its group's next tile between its MFMAs (the descriptor
     // after MFMA 0, block j after MFMA 8j + 1). A group's periods run in four kinds:
     //  * first (m = 0): K Q^T only, as there is no tile -1 for a P V;
@@ -437,7 +446,7 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     //    still read those tiles) but no MFMAs,
     // where G is the number of tiles any row of the group sees: num_tiles, or fewer for the group of
     // earlier rows on a causal diagonal, whose tiles past those rows' diagonal it skips. Both groups
-    // run num_tiles + 1 periods of two barriers each.
+    // run num_tiles + 1 periods of one barrier each.
     int group_tiles = num_tiles;
     if (a.causal) {
       const int last = q0 + (group + 1) * kLoadWaves * kRowsPerWave - 1 + a.causal_offset;
@@ -474,14 +483,13 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
         if constexpr (kGroup == 0) {
           if constexpr (kMode == kFirstT::value) prefetch_qk(slot);
           mfma();
-          phase_barrier();
           if constexpr (kDoQk) {
             // The next MFMA phase's first fragments (V(m), published by the barrier that ended
-            // half-period 2m), read first so their latency hides behind the softmax.
+            // period m - 1), read first so their latency hides behind the softmax.
             prefetch(slot + 1);
             softmax_phase(m);
           }
-          wait_vmcnt<kPendingK>();  // K(m + 1), first read in half-period 2m + 2
+          wait_vmcnt<kPendingK>();  // K(m + 1), first read in period m + 1
           phase_barrier();
         } else {
           if constexpr (kMode == kFirstT::value) prefetch_qk(slot);
@@ -489,9 +497,8 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
             prefetch(slot);
             softmax_phase(m - 1);
           }
-          wait_vmcnt<kPendingV>();  // V(m), first read in half-period 2m + 1
-          phase_barrier();
           mfma();
+          wait_vmcnt<kPendingV>();  // V(m + 1), first read in period m + 1
           phase_barrier();
         }
       };
