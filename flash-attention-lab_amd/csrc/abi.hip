@@ -61,12 +61,10 @@ int64_t pages_per_split(int max_seqlen, int num_splits, int page_size) {
   return keys / page_size + 2;
 }
 
-// Largest power of two (at most 128) whose split workgroups all fit on the GPU at once
-// (resident_per_cu per CU; the FL_KNOB_DECODE_WG_PER_CU knob overrides it) while each
-// split of the longest possible sequence keeps at least 512 keys. One wave of workgroups that
-// fills the GPU streams the cache with no tail; measured on MI355X at 32K keys, this beat aiming
-// for two or more workgroups per resident slot, and splits of 256 keys (B=1 MHA, 128 splits)
-// lost about 1% to 512-key ones (64 splits). When that leaves fewer workgroups than a quarter of
+// Largest power of two (at most 128) whose split workgroups all fit the planned slots at once
+// (planned_per_cu per CU, below) while each split of the longest possible sequence keeps at
+// least 512 keys. One wave of workgroups that fills the GPU streams the cache with no tail;
+// measured on MI355X at 32K keys, this beat aiming for two or more workgroups per slot. When that leaves fewer workgroups than a quarter of
 // the resident slots (a short cache or few sequences and heads, e.g. one 8K-key sequence with 8
 // KV heads: 32 workgroups), splits go down to 64 keys: many short splits beat a few long ones
 // that leave most CUs idle. The matrix-core kernel (one resident workgroup per CU, four 32-key
@@ -101,6 +99,21 @@ int choose_num_splits(int64_t workgroups, int max_seqlen, int cu_count, int resi
 constexpr int64_t kMinSpanWorkgroups = 256;
 // Keys per split the vector kernel prefers when a cache is long enough to fill the GPU with them.
 constexpr int kLongSplitKeys = 2048;
+
+// Split workgroups per CU the plan aims for (the FL_KNOB_DECODE_WG_PER_CU knob overrides it). The
+// vector kernel with one query head per workgroup (MHA), two batches of rows in flight per lane,
+// streams fastest with one workgroup per CU on a contiguous cache: bf16 at 32K keys, B=8 MHA 609
+// us with 4 splits against 639 with 16 (five per CU), B=4 309 against 333, B=16 1,196 against
+// 1,296; B=8 at 8K keys 160 against 174, at 4K keys (B=32) 317 against 339; fp16, fp32 and D = 64
+// alike. On a paged cache each row address waits for a block-table lookup in LDS, and a second
+// workgroup per CU hides it: B=8 MHA with 16-row pages 638 us at two per CU, 670 at five, 740 at
+// one. Workgroups of several query heads keep the residency figure (three per CU): at B=8 with a
+// group of 2, 167 us against 176 at one per CU; with a group of 4, 174 at either. The matrix-core
+// kernel fits one per CU.
+int planned_per_cu(const fl_decode_params* p, const fl::DecodeLayout& layout) {
+  if (layout.mfma || layout.heads_per_wg > 1) return layout.resident_per_cu;
+  return p->block_tables != nullptr ? (layout.resident_per_cu < 2 ? layout.resident_per_cu : 2) : 1;
+}
 
 // KV heads per workgroup for a decode with num_splits splits: the widest span the layout allows
 // that still yields kMinSpanWorkgroups workgroups, else 1. fl_decode_plan and fl_decode both
@@ -372,19 +385,18 @@ int fl_decode_plan(const fl_decode_params* p, int32_t requested_splits, int32_t 
     int64_t planned_wg = 0;
     for (int s = layout.kv_span; s >= 1; s /= 2) {
       const int64_t wg = static_cast<int64_t>(p->batch) * (p->heads_kv / s) * (group / layout.wg_heads);
-      n = choose_num_splits(wg, p->max_seqlen, cu_count, layout.resident_per_cu, layout.mfma != 0);
+      n = choose_num_splits(wg, p->max_seqlen, cu_count, planned_per_cu(p, layout), layout.mfma != 0);
       planned_wg = wg * n;
       if (s == 1 || planned_wg >= kMinSpanWorkgroups) break;
     }
     // MHA at head_dim 128, 16-bit (the measured case), with at most two workgroups per CU that
-    // way (few sequences, a long cache): at least 16 splits of at least kLongSplitKeys keys instead, if some span then still
-    // gives every CU a workgroup. B=1, 32 KV heads, 32K keys: 16 splits of 2 KV heads 6.05-6.12
-    // TB/s against 5.99-6.03 for 64 splits of 4; at B=2 and 4 (four workgroups per CU) the longer
-    // splits measured 0.2-0.3% slower, so they are not used there.
+    // way (few sequences, a long cache): at least 16 splits of at least kLongSplitKeys keys
+    // instead, if some span then still gives every CU a workgroup. B=1, 32 KV heads, 32K keys: 16
+    // splits of 2 KV heads 83.2-83.7 us against 84.7-85.3 for 32 splits of 4.
     const int cus = cu_count > 0 ? cu_count : 256;
     if (!layout.mfma && group == 1 && p->head_dim == 128 && p->dtype != FL_DTYPE_F32 &&
         planned_wg <= 2 * cus) {
-      const int64_t capacity = resident_capacity(cu_count, layout.resident_per_cu);
+      const int64_t capacity = resident_capacity(cu_count, planned_per_cu(p, layout));
       for (int s = layout.kv_span; s >= 1; s /= 2) {
         const int64_t wg = static_cast<int64_t>(p->batch) * (p->heads_kv / s) * (group / layout.wg_heads);
         const int m = largest_splits(wg, p->max_seqlen, capacity, kLongSplitKeys);

@@ -77,13 +77,13 @@ def test_version():
 
 @pytest.mark.parametrize(
     "batch,heads,heads_kv,expected_splits",
-    # The largest power of two whose workgroups all fit at once, with >= 512 keys per split. MHA
-    # (vector kernel): 4 KV heads per workgroup, 5 resident per CU (1280): 64 x 16 workgroups at
-    # B=8; at B=1 that rule gives 8 x 64 (two per CU), and long splits win there: 16 splits of
-    # 2048 keys, 2 KV heads per workgroup (256 workgroups). GQA with 4 query heads per KV head
-    # (matrix-core kernel): one KV head per workgroup, 1 resident per CU (256): 64 x 4.
-    [(1, 32, 32, 16), (8, 32, 32, 16), (8, 32, 8, 4)],
-    ids=["B1-MHA", "B8-MHA", "B8-GQA"],
+    # The largest power of two whose workgroups fill the planned slots at once, with >= 512 keys
+    # per split. MHA (vector kernel, contiguous cache): 4 KV heads per workgroup, one planned per
+    # CU (256 slots): 64 x 4 workgroups at B=8, 32 x 8 at B=4; at B=1 that rule gives 8 x 32, and
+    # 16 splits of 2048 keys with 2 KV heads per workgroup (256 workgroups) win there. GQA with 4
+    # query heads per KV head (matrix-core kernel): one KV head per workgroup, 1 per CU: 64 x 4.
+    [(1, 32, 32, 16), (4, 32, 32, 8), (8, 32, 32, 4), (8, 32, 8, 4)],
+    ids=["B1-MHA", "B4-MHA", "B8-MHA", "B8-GQA"],
 )
 def test_decode_plan_on_256_cus(batch, heads, heads_kv, expected_splits):
     splits, ws = _hip.decode_plan(batch, heads, heads_kv, 128, 32768, torch.bfloat16)
@@ -123,7 +123,8 @@ def test_decode_plan_requested_and_inplace():
     )
     # Splits keep >= 512 keys while that leaves enough workgroups; with few workgroups (one
     # sequence, 8 KV heads) they go down to 64 keys, and a cache under 128 keys is not split.
-    assert _hip.decode_plan(8, 32, 32, 128, 4096, torch.bfloat16)[0] == 8  # 512 keys each
+    # B=8 MHA at 4K keys: 64 workgroups of 4 KV heads per split, one per CU: 4 splits.
+    assert _hip.decode_plan(8, 32, 32, 128, 4096, torch.bfloat16)[0] == 4  # 1024 keys each
     assert _hip.decode_plan(1, 8, 8, 128, 1000, torch.bfloat16)[0] == 8  # 125 keys each
     assert _hip.decode_plan(1, 8, 8, 128, 100, torch.bfloat16)[0] == 1
     assert _hip.decode_plan(1, 8, 8, 128, 128, torch.bfloat16)[0] == 2
