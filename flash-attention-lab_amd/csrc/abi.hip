@@ -127,6 +127,36 @@ int decode_span(const fl_decode_params* p, const fl::DecodeLayout& layout, int n
   return 1;
 }
 
+// Matrix-core kernel with four KV heads per workgroup, one per wave: the workgroup's loads for a
+// key then cover the four heads' rows, one contiguous 1 KiB segment at D = 128 (one KV head per
+// workgroup reads 256-byte rows at the cache's row stride). It needs enough work for one
+// workgroup per CU with long splits: bf16, 32K keys, B=8 with 8 KV heads 169.4 us (16 splits)
+// against 174.2 (one KV head per workgroup, 4 splits); B=4 92.2 against 95.0; B=16 at 8K keys
+// 91.0 against 94.5; D = 64 with 8 query heads per KV head 91.4 against 99.5; at B=1 and 2 (too
+// few workgroups unless the splits get short) it loses or ties. fl_decode_plan and fl_decode both
+// derive it from the same parameters.
+constexpr int kMfmaSpan = 4;
+constexpr int kMfmaSpanSplitKeys = 1024;
+int mfma_span(const fl_decode_params* p, const fl::DecodeLayout& layout, int num_splits) {
+  if (!layout.mfma || p->heads_kv % kMfmaSpan != 0) return 1;
+  const int64_t wg = static_cast<int64_t>(p->batch) * (p->heads_kv / kMfmaSpan) * num_splits;
+  const bool long_splits = num_splits == 1 || p->max_seqlen / num_splits >= kMfmaSpanSplitKeys;
+  return wg >= kMinSpanWorkgroups && long_splits ? kMfmaSpan : 1;
+}
+
+// Split count for the four-heads-per-workgroup layout: the largest power of two that keeps one
+// workgroup per CU and splits of at least kMfmaSpanSplitKeys keys; 0 if that does not fill the
+// CUs (the one-head layout's plan applies then).
+int mfma_span_splits(const fl_decode_params* p, const fl::DecodeLayout& layout, int cu_count) {
+  if (!layout.mfma || p->heads_kv % kMfmaSpan != 0) return 0;
+  const int64_t cus = cu_count > 0 ? cu_count : 256;
+  const int64_t groups = static_cast<int64_t>(p->batch) * (p->heads_kv / kMfmaSpan);
+  int n = 1;
+  while (n < fl::kMaxSplits && groups * 2 * n <= cus && p->max_seqlen / (2 * n) >= kMfmaSpanSplitKeys)
+    n *= 2;
+  return mfma_span(p, layout, n) == kMfmaSpan ? n : 0;
+}
+
 int check_decode_shape(const fl_decode_params* p) {
   if (p == nullptr) return fail(FL_ERR_INVALID, "null decode parameters");
   if (p->block_tables != nullptr && (p->page_size <= 0 || p->num_blocks <= 0))
@@ -212,6 +242,7 @@ int decode_call(const fl_decode_params* p, float* workspace, size_t workspace_by
   a.head_chunks = head_chunks;
   a.kv_span = decode_span(p, layout, p->num_splits);
   a.mfma = layout.mfma;
+  a.mfma_span = mfma_span(p, layout, p->num_splits);
   a.block_tables = p->block_tables;
   a.block_tables_stride = p->block_tables_stride;
   a.page_size = p->page_size;
@@ -389,6 +420,7 @@ int fl_decode_plan(const fl_decode_params* p, int32_t requested_splits, int32_t 
       planned_wg = wg * n;
       if (s == 1 || planned_wg >= kMinSpanWorkgroups) break;
     }
+    if (const int n4 = mfma_span_splits(p, layout, cu_count)) n = n4;
     // MHA at head_dim 128, 16-bit (the measured case), with at most two workgroups per CU that
     // way (few sequences, a long cache): at least 16 splits of at least kLongSplitKeys keys
     // instead, if some span then still gives every CU a workgroup. B=1, 32 KV heads, 32K keys: 16

@@ -13,8 +13,12 @@
 //    Q^T the B operand in registers: one query head per column, columns past the group zero), and
 //    the output as O^T = V^T P^T (V^T read with ds_read_b64_tr_b16). Lane l holds query head
 //    l % 32 and 16 of a tile's 32 keys, so softmax state and output rescaling are per lane.
-//  * Workgroup: 4 waves, one KV head with all of its query heads (up to 32), one split. Wave w takes
-//    the split's 32-key tiles w, w + 4, w + 8, ... (the four waves read neighbouring rows).
+//  * Workgroup: 4 waves and one split, in one of two layouts (mfma_span, chosen on the host): one
+//    KV head with all of its query heads (up to 32), wave w taking the split's 32-key tiles w,
+//    w + 4, w + 8, ... (the four waves read neighbouring rows); or four adjacent KV heads, wave w
+//    taking KV head 4 q + w over all of the split's tiles, so that for each key the workgroup
+//    reads the four heads' rows, one contiguous 1 KiB segment at D = 128. The second needs more
+//    work to fill the GPU and is used when there is enough of it.
 //  * Each wave loads its tiles into registers with 16-byte non-temporal loads (every load
 //    instruction moves whole rows: four 256-byte rows at D = 128), one tile ahead, and writes each
 //    tile into its own LDS buffer (K 8 KiB + V 8 KiB at D = 128) in the XOR-swizzled layout the
@@ -28,7 +32,8 @@
 //    blocks, read from the table in global memory), clamped to the pool, and every lane computes
 //    the address of the row it loads. The keys and their order are the contiguous cache's, so the
 //    results are bitwise the same.
-//  * At the end the four waves are merged in order through LDS, and the workgroup writes o and lse
+//  * At the end the four waves are merged in order through LDS (one KV head; with four, each wave's
+//    state is its own head's and is written as it is), and the workgroup writes o and lse
 //    (one split) or its unnormalized partial output and (max, sum), which decode.hip's merge pass
 //    combines. No atomics: results are bitwise reproducible for a given split count.
 #include "gfx950.hpp"
@@ -90,8 +95,10 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
   int w = blockIdx.x;
   const int split = w % a.num_splits;
   w /= a.num_splits;
-  const int hkv = w % a.heads_kv;
-  const int b = w / a.heads_kv;
+  const int span = a.mfma_span;  // 1, or 4: wave w takes KV head 4 q + w over all the split's tiles
+  const int hq = w % (a.heads_kv / span);
+  const int b = w / (a.heads_kv / span);
+  const int hkv = span == 1 ? hq : hq * span + wave;
   const int group = a.group;  // <= kCols (checked on the host)
   const int h0 = hkv * group;
 
@@ -103,7 +110,7 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
   const int k_begin = split * per_split;
   const int k_end = min(len, k_begin + per_split);
   const int tiles = k_begin < k_end ? (k_end - k_begin + kTileKeys - 1) / kTileKeys : 0;
-  const int my_tiles = tiles > wave ? (tiles - wave + kWaves - 1) / kWaves : 0;
+  const int my_tiles = span == 1 ? (tiles > wave ? (tiles - wave + kWaves - 1) / kWaves : 0) : tiles;
 
   // Q^T, the B operand: lane (col, half) holds q[h0 + col][16 ks + 8 half .. + 7], zero past the
   // group.
@@ -158,7 +165,9 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
     }
   };
   char* wave_lds = reinterpret_cast<char*>(smem) + wave * kWaveBytes<D>;
-  auto tile_start = [&](int i) __attribute__((always_inline)) { return k_begin + (wave + kWaves * i) * kTileKeys; };
+  auto tile_start = [&](int i) __attribute__((always_inline)) {
+    return k_begin + (span == 1 ? wave + kWaves * i : i) * kTileKeys;
+  };
   using Regs = u32x4[2 * kLoads<D>];  // K loads, then V loads
   auto load_tile = [&](int i, Regs& r) __attribute__((always_inline)) {
     const int t0 = tile_start(i);
@@ -283,24 +292,37 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
     }
   }
   __syncthreads();
-  for (int idx = tid; idx < group * D; idx += kThreads) {
-    const int g = idx / D;
-    const int d = idx - g * D;
+  // Span 1: the four waves' states of one KV head are merged in wave order. Span 4: each wave's
+  // state is its own KV head's and is written as it is.
+  const int outs = span == 1 ? group * D : kWaves * group * D;
+  for (int idx = tid; idx < outs; idx += kThreads) {
+    const int wv0 = span == 1 ? 0 : idx / (group * D);
+    const int r = idx - wv0 * group * D;
+    const int g = r / D;
+    const int d = r - g * D;
     float mm = -INFINITY;
-#pragma unroll
-    for (int wv = 0; wv < kWaves; ++wv) mm = fmaxf(mm, red_m[wv * kCols + g]);
     float num = 0.f;
     float den = 0.f;
+    if (span == 1) {
 #pragma unroll
-    for (int wv = 0; wv < kWaves; ++wv) {
-      const float mw = red_m[wv * kCols + g];
-      if (mw != -INFINITY) {
-        const float f = exp2_fast(mw - mm);
-        num += red_o[(wv * kCols + g) * kRedPitch<D> + d] * f;
-        den += red_l[wv * kCols + g] * f;
+      for (int wv = 0; wv < kWaves; ++wv) mm = fmaxf(mm, red_m[wv * kCols + g]);
+#pragma unroll
+      for (int wv = 0; wv < kWaves; ++wv) {
+        const float mw = red_m[wv * kCols + g];
+        if (mw != -INFINITY) {
+          const float f = exp2_fast(mw - mm);
+          num += red_o[(wv * kCols + g) * kRedPitch<D> + d] * f;
+          den += red_l[wv * kCols + g] * f;
+        }
+      }
+    } else {
+      mm = red_m[wv0 * kCols + g];
+      if (mm != -INFINITY) {
+        num = red_o[(wv0 * kCols + g) * kRedPitch<D> + d];
+        den = red_l[wv0 * kCols + g];
       }
     }
-    const int h = h0 + g;
+    const int h = (span == 1 ? h0 : (hq * span + wv0) * group) + g;
     if (a.num_splits == 1) {
       uint16_t* orow = static_cast<uint16_t*>(a.o) + b * a.o_bs + h * a.o_hs;
       orow[d] = E::from_float(den > 0.f ? num / den : 0.f);
@@ -318,7 +340,7 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
 
 template <typename Tag, int D>
 hipError_t launch_typed(const DecodeArgs& args, hipStream_t stream) {
-  const dim3 grid(args.batch * args.heads_kv * args.num_splits);
+  const dim3 grid(args.batch * (args.heads_kv / args.mfma_span) * args.num_splits);
   if (args.block_tables == nullptr) {
     hipLaunchKernelGGL((decode_mfma_kernel<Tag, D, kContiguous>), grid, dim3(kThreads), 0, stream, args);
   } else if (!args.page_table_global) {

@@ -59,6 +59,9 @@ struct DecodeArgs {
   // The matrix-core split kernel (decode_mfma.hip) serves the call: one workgroup per KV head and
   // split, with all `group` query heads (kv_span and head_chunks then only shape the merge pass).
   int mfma;
+  // Matrix-core kernel: KV heads per workgroup, 1 (the four waves share one KV head's tiles) or 4
+  // (wave w takes KV head 4 q + w over all of the split's tiles).
+  int mfma_span;
 };
 
 // How the decode kernels find cache rows: contiguous cache, paged cache with the split's block

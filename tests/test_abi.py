@@ -81,9 +81,11 @@ def test_version():
     # per split. MHA (vector kernel, contiguous cache): 4 KV heads per workgroup, one planned per
     # CU (256 slots): 64 x 4 workgroups at B=8, 32 x 8 at B=4; at B=1 that rule gives 8 x 32, and
     # 16 splits of 2048 keys with 2 KV heads per workgroup (256 workgroups) win there. GQA with 4
-    # query heads per KV head (matrix-core kernel): one KV head per workgroup, 1 per CU: 64 x 4.
-    [(1, 32, 32, 16), (4, 32, 32, 8), (8, 32, 32, 4), (8, 32, 8, 4)],
-    ids=["B1-MHA", "B4-MHA", "B8-MHA", "B8-GQA"],
+    # query heads per KV head (matrix-core kernel): four KV heads per workgroup (one per wave),
+    # one per CU, splits of >= 1024 keys: 16 x 16 at B=8; at B=1 that cannot fill the CUs, so one
+    # KV head per workgroup: 8 x 32.
+    [(1, 32, 32, 16), (4, 32, 32, 8), (8, 32, 32, 4), (8, 32, 8, 16), (1, 32, 8, 32)],
+    ids=["B1-MHA", "B4-MHA", "B8-MHA", "B8-GQA", "B1-GQA"],
 )
 def test_decode_plan_on_256_cus(batch, heads, heads_kv, expected_splits):
     splits, ws = _hip.decode_plan(batch, heads, heads_kv, 128, 32768, torch.bfloat16)
@@ -93,17 +95,17 @@ def test_decode_plan_on_256_cus(batch, heads, heads_kv, expected_splits):
 
 def test_decode_plan_routes_by_group(knobs):
     # Groups of 4 to 32 query heads per KV head (bf16/fp16, head_dim 128) go to the matrix-core
-    # kernel, one KV head per workgroup and one workgroup per CU: B=8 with 8 KV heads takes 4
+    # kernel, four KV heads per workgroup and one workgroup per CU: B=8 with 8 KV heads takes 16
     # splits (256 workgroups) whatever the group. Smaller groups and fp32 stay on the vector
     # kernel, and the decode_mfma_min_group knob moves the threshold.
     plan = lambda heads, dtype=torch.bfloat16: _hip.decode_plan(8, heads, 8, 128, 32768, dtype)[0]
-    assert plan(32) == plan(64) == plan(256) == 4  # groups 4, 8, 32
+    assert plan(32) == plan(64) == plan(256) == 16  # groups 4, 8, 32
     assert plan(16) == 32  # group 2: vector kernel, 4 KV heads per workgroup, 3 per CU
-    assert plan(32, torch.float16) == 4
+    assert plan(32, torch.float16) == 16
     assert plan(32, torch.float32) == 16  # 2 KV heads per workgroup, 3 per CU
     # head_dim 64 (128-byte rows): from 8 query heads per KV head.
     assert _hip.decode_plan(8, 32, 8, 64, 32768, torch.bfloat16)[0] == 32
-    assert _hip.decode_plan(8, 64, 8, 64, 32768, torch.bfloat16)[0] == 4
+    assert _hip.decode_plan(8, 64, 8, 64, 32768, torch.bfloat16)[0] == 16
     # Short caches: as many splits as fill the CUs with >= 128 keys each.
     assert _hip.decode_plan(1, 32, 8, 128, 8448, torch.bfloat16)[0] == 32
     assert _hip.decode_plan(1, 32, 8, 128, 2048, torch.bfloat16)[0] == 16
@@ -111,7 +113,9 @@ def test_decode_plan_routes_by_group(knobs):
     knobs("decode_mfma_min_group", 1000)
     assert plan(32) == 32
     knobs("decode_mfma_min_group", 1)
-    assert plan(8) == 4
+    assert plan(8) == 16
+    # One KV head per workgroup where four cannot fill the CUs with splits of >= 1024 keys.
+    assert _hip.decode_plan(2, 32, 8, 128, 32768, torch.bfloat16)[0] == 16
 
 
 def test_decode_plan_requested_and_inplace():
