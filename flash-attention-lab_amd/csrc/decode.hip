@@ -541,14 +541,16 @@ hipError_t launch_type(const DecodeArgs& args, DType dtype, int head_dim, int k_
 }  // namespace decode
 
 // Smallest GQA group the matrix-core kernel serves (the FL_KNOB_DECODE_MFMA_MIN_GROUP knob
-// overrides it; a value above kMaxDecodeMfmaHeads turns the kernel off). Measured at 32K keys,
-// B=8, 8 KV heads: at D = 128 it beats the vector kernel from 4 query heads per KV head (6.18 vs
-// 6.0 TB/s fp16; 2 heads: 6.09 vs 6.38); at D = 64 (128-byte rows) from 8 (5.34 vs 4.1; at 4,
-// 5.35-5.39 vs 5.30-5.63).
+// overrides it; a value above kMaxDecodeMfmaHeads turns the kernel off): 4 query heads per KV head
+// at D = 128 and 64. With 4, bf16 at 32K keys: D = 128, B=8 169 vs 172-175 us, B=1 33.7 vs 38.2;
+// D = 64, B=8 86.4 vs 93.8, B=4 50.7 vs 56.2, B=1 23.4 vs 24.4, one 8.4K-key sequence 14.9 vs
+// 18.0. With 2 it is mixed (D = 128: B=2 54.3 vs 49.3, B=4 89.3 vs 90.6; D = 64: B=2 33.7 vs
+// 30.4, B=8 85.7 vs 89.5), so groups of 2 stay on the vector kernel.
 int decode_mfma_min_group(int head_dim) {
+  (void)head_dim;
   const int v = knob(FL_KNOB_DECODE_MFMA_MIN_GROUP);
   if (v >= 1) return v;
-  return head_dim == 64 ? 8 : 4;
+  return 4;
 }
 
 DecodeLayout decode_layout(DType dtype, int head_dim, int heads_kv, int group) {

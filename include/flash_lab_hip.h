@@ -177,7 +177,7 @@ int fl_mfma_tile_test(const void* a, const void* b, float* c, int32_t k, int32_t
  *                                  (default 256; 0 = always, 2^30 = never).
  *   FL_KNOB_DECODE_MFMA_MIN_GROUP  [1, 2^20]: smallest GQA group the
  *                                  matrix-core decode kernel takes (default
- *                                  4 at head_dim 128, 8 at 64; above 32 =
+ *                                  4 at head_dim 128 and 64; above 32 =
  *                                  never).
  *   FL_KNOB_DECODE_WG_PER_CU       [1, 64]: resident split workgroups per CU
  *                                  that fl_decode_plan assumes.

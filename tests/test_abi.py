@@ -103,8 +103,8 @@ def test_decode_plan_routes_by_group(knobs):
     assert plan(16) == 32  # group 2: vector kernel, 4 KV heads per workgroup, 3 per CU
     assert plan(32, torch.float16) == 16
     assert plan(32, torch.float32) == 16  # 2 KV heads per workgroup, 3 per CU
-    # head_dim 64 (128-byte rows): from 8 query heads per KV head.
-    assert _hip.decode_plan(8, 32, 8, 64, 32768, torch.bfloat16)[0] == 32
+    # head_dim 64 (128-byte rows): from 4 query heads per KV head as well.
+    assert _hip.decode_plan(8, 32, 8, 64, 32768, torch.bfloat16)[0] == 16
     assert _hip.decode_plan(8, 64, 8, 64, 32768, torch.bfloat16)[0] == 16
     # Short caches: as many splits as fill the CUs with >= 128 keys each.
     assert _hip.decode_plan(1, 32, 8, 128, 8448, torch.bfloat16)[0] == 32
