@@ -61,16 +61,6 @@ int64_t pages_per_split(int max_seqlen, int num_splits, int page_size) {
   return keys / page_size + 2;
 }
 
-// Largest power of two (at most 128) whose split workgroups all fit the planned slots at once
-// (planned_per_cu per CU, below) while each split of the longest possible sequence keeps at
-// least 512 keys. One wave of workgroups that fills the GPU streams the cache with no tail;
-// measured on MI355X at 32K keys, this beat aiming for two or more workgroups per slot. When that leaves fewer workgroups than a quarter of
-// the resident slots (a short cache or few sequences and heads, e.g. one 8K-key sequence with 8
-// KV heads: 32 workgroups), splits go down to 64 keys: many short splits beat a few long ones
-// that leave most CUs idle. The matrix-core kernel (one resident workgroup per CU, four 32-key
-// tiles per pass) takes the largest count that fills the CUs with at least 128 keys per split: on
-// one 8,448-key sequence with 8 KV heads, 32 splits of 264 keys took 14.8 us against 17.4 us for
-// 16 of 528, and at 32K keys 32 splits were the fastest too (29.3 us).
 // Largest power of two (at most 128) whose workgroups fit `capacity` and whose splits keep at
 // least min_keys keys.
 int largest_splits(int64_t workgroups, int max_seqlen, int64_t capacity, int min_keys) {
@@ -85,6 +75,17 @@ int64_t resident_capacity(int cu_count, int resident_per_cu) {
   return static_cast<int64_t>(resident_per_cu) * (cu_count > 0 ? cu_count : 256);
 }
 
+// Largest power of two (at most 128) whose split workgroups all fit the planned slots at once
+// (resident_per_cu per CU, the caller's planned_per_cu figure) while each split of the longest
+// possible sequence keeps at least 512 keys. One wave of workgroups that fills the GPU streams
+// the cache with no tail; measured on MI355X at 32K keys, this beat aiming for two or more
+// workgroups per slot. When that leaves fewer workgroups than a quarter of the slots (a short
+// cache or few sequences and heads, e.g. one 8K-key sequence with 8 KV heads: 32 workgroups),
+// splits go down to 64 keys: many short splits beat a few long ones that leave most CUs idle.
+// The matrix-core kernel (one resident workgroup per CU, four 32-key tiles per pass) takes the
+// largest count that fills the CUs with at least 128 keys per split: on one 8,448-key sequence
+// with 8 KV heads, 32 splits of 264 keys took 14.8 us against 17.4 us for 16 of 528, and at 32K
+// keys 32 splits were the fastest too (29.3 us).
 int choose_num_splits(int64_t workgroups, int max_seqlen, int cu_count, int resident_per_cu,
                       bool mfma) {
   const int64_t capacity = resident_capacity(cu_count, resident_per_cu);
