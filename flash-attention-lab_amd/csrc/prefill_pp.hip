@@ -231,6 +231,13 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
       const char* p = reinterpret_cast<const char*>(my_base) + (inside ? t * tile_bytes : 0);
       return buffer_words(p, bytes);
     };
+    // The same for a tile t >= 0 whose first row is at p = my_base + t tile_bytes, which the periods
+    // carry from one to the next: half the scalar instructions, issued between two MFMAs. A tile
+    // past the last one gets size 0, so its address is never formed.
+    auto tile_words_at = [&](int t, const char* p) -> u32x4s {
+      const int d = num_tiles - 1 - t;
+      return buffer_words(p, d > 0 ? full_bytes : d == 0 ? last_bytes : 0u);
+    };
     // Block j of the group's tile (descriptor `w`) into ring slot kSlot.
     auto issue_block = [&](u32x4s w, int slot, auto j_tag) {
       constexpr int j = decltype(j_tag)::value;
@@ -461,6 +468,8 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
       // Group 0 loads K(m + kStages - 1) into slot (m - 1) % kStages, group 1 V(m + kStages - 2)
       // into slot (m - 2) % kStages.
       constexpr int kLead = kGroup == 0 ? kStages - 1 : kStages - 2;
+      // First row of tile m + kLead, the tile that period m loads.
+      const char* lead_tile = reinterpret_cast<const char*>(my_base) + kLead * tile_bytes;
       auto period = [&](int m, int slot, auto mode_tag) {
         constexpr int kMode = decltype(mode_tag)::value;
         constexpr bool kDoPv = kMode == kFullT::value || kMode == kLastT::value;
@@ -468,7 +477,10 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
         u32x4s w;
         auto hook = [&](auto i_tag) {
           constexpr int i = decltype(i_tag)::value;
-          if constexpr (i == 0) w = tile_words(m + kLead);
+          if constexpr (i == 0) {
+            w = tile_words_at(m + kLead, lead_tile);
+            lead_tile += tile_bytes;
+          }
           if constexpr (i % 8 == 1 && i / 8 < kDmaPerWave) {
             issue_block(w, slot + kLead, std::integral_constant<int, i / 8>{});
           }
