@@ -13,6 +13,9 @@
 //    Q^T the B operand in registers: one query head per column, columns past the group zero), and
 //    the output as O^T = V^T P^T (V^T read with ds_read_b64_tr_b16). Lane l holds query head
 //    l % 32 and 16 of a tile's 32 keys, so softmax state and output rescaling are per lane.
+//    The online softmax keeps a lazily moved reference point (as prefill_pp.hip does): a tile's
+//    probabilities are taken against it, and only when a lane's sum exceeds 2^15 is the row max
+//    taken and O and l rescaled, so most tiles skip the max and the rescale of O.
 //  * Workgroup: 4 waves and one split, in one of two layouts (mfma_span, chosen on the host): one
 //    KV head with all of its query heads (up to 32), wave w taking the split's 32-key tiles w,
 //    w + 4, w + 8, ... (the four waves read neighbouring rows); or four adjacent KV heads, wave w
@@ -34,8 +37,9 @@
 //    results are bitwise the same.
 //  * At the end the four waves are merged in order through LDS (one KV head; with four, each wave's
 //    state is its own head's and is written as it is), and the workgroup writes o and lse
-//    (one split) or its unnormalized partial output and (max, sum), which decode.hip's merge pass
-//    combines. No atomics: results are bitwise reproducible for a given split count.
+//    (one split) or its unnormalized partial output and (reference point, sum), which decode.hip's
+//    merge pass combines as it would (max, sum). No atomics: results are bitwise reproducible for a
+//    given split count.
 #include "gfx950.hpp"
 #include "launch.hpp"
 #include "prefill_tile.hpp"
@@ -59,6 +63,11 @@ constexpr int kTileKeys = 32;  // one MFMA key block
 #endif
 constexpr int kAhead = FL_DMFMA_AHEAD;  // tiles in flight in registers per wave
 constexpr float kLn2 = 0.693147180559945309f;
+// Largest lane sum of a tile's probabilities (16 of them) kept without moving the reference point.
+constexpr float kSumLimit = 32768.f;
+// Reference point before the first tile: finite, so the first tile's probabilities overflow and
+// take the path that moves it, and masked scores (-inf) still give 0.
+constexpr float kNoRef = -1e30f;
 
 template <int D>
 constexpr int kTileBytes = kTileKeys * D * 2;  // one tensor's tile
@@ -68,8 +77,9 @@ template <int D>
 constexpr int kWaveBytes = 2 * kTileBytes<D>;  // a wave's LDS tile: K, then V
 template <int D>
 constexpr int kLdsBytes = kWaves * kWaveBytes<D>;
-// Final merge through LDS (reusing the tile buffers): (max, sum) per wave and column, then each
-// wave's output rows with one float of padding (conflict-free stores from the 32 columns).
+// Final merge through LDS (reusing the tile buffers): (reference point, sum) per wave and column,
+// then each wave's output rows with one float of padding (conflict-free stores from the 32
+// columns).
 template <int D>
 constexpr int kRedPitch = D + 1;
 template <int D>
@@ -192,8 +202,12 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
   f32x16 o[D / 32];
 #pragma unroll
   for (int nb = 0; nb < D / 32; ++nb) o[nb] = f32x16{};
-  float m = -INFINITY;  // running max over this wave's keys for the lane's head (log2 units)
-  float l = 0.f;        // the lane's part of the running sum (its 16 keys of each tile)
+  // Reference point of o and l for the lane's head (log2 units, the same in both halves of a
+  // column; kNoRef until the first tile). Probabilities are 2^(s scale_log2 - ref), and the point
+  // moves only when a lane's sum of them exceeds kSumLimit, so each stays at most 2^15 (fp16
+  // reaches 65504).
+  float ref = kNoRef;
+  float l = 0.f;  // the lane's part of the running sum (its 16 keys of each tile)
   const float sl2 = a.scale_log2;
 
   // Tile i from register set r: into LDS, fragments back, the set refilled with tile i + kAhead,
@@ -228,24 +242,37 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
         if (acc_key(j, 0) > lim) s[j] = -INFINITY;
       }
     }
-    float mx = s[0];
-#pragma unroll
-    for (int j = 1; j < 16; ++j) mx = fmaxf(mx, s[j]);
-    mx = max_halves(mx) * sl2;  // scale_log2 > 0, so the max commutes with it
-    const float m_new = fmaxf(m, mx);
-    const float ref = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2_fast(m - ref);  // 0 on the first tile (m = -inf)
+    // Probabilities against the current reference point; it moves (and O and l are rescaled)
+    // only when a lane's sum exceeds kSumLimit, which the first tile always does (ref starts at
+    // kNoRef). The row max is therefore not needed on most tiles, and O, which the compiler keeps in
+    // accumulator registers, is not touched by VALU work between them.
     f32x16 p;
-    float rs = 0.f;
+    auto probabilities = [&]() __attribute__((always_inline)) {
+      float r = 0.f;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      p[j] = exp2_fast(fmaf(s[j], sl2, -ref));
-      rs += p[j];
+      for (int j = 0; j < 16; ++j) {
+        p[j] = exp2_fast(fmaf(s[j], sl2, -ref));
+        r += p[j];
+      }
+      return r;
+    };
+    float rs = probabilities();
+    if (wave_any(rs > kSumLimit)) {
+      float mx = s[0];
+#pragma unroll
+      for (int j = 1; j < 16; ++j) mx = fmaxf(mx, s[j]);
+      // scale_log2 > 0, so the max commutes with it; every row sees a valid key of the tile.
+      const float moved = fmaxf(ref, max_halves(mx) * sl2);
+      const float alpha = exp2_fast(ref - moved);  // 0 on the first tile
+      ref = moved;
+      if (wave_any(alpha != 1.f)) {
+#pragma unroll
+        for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
+      }
+      l *= alpha;
+      rs = probabilities();
     }
-    l = l * alpha + rs;
-    m = m_new;
-#pragma unroll
-    for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
+    l += rs;
     const u32x4 p0 = p_frag<Tag, 0>(p);
     const u32x4 p1 = p_frag<Tag, 1>(p);
 #pragma unroll
@@ -280,7 +307,8 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
   float* red_o = red_l + kWaves * kCols;          // [kWaves][kCols][kRedPitch]
   const float lt = sum_halves(l);
   if (half == 0) {
-    red_m[wave * kCols + col] = m;
+    // A wave that saw no key (l = 0, ref still kNoRef) records -inf, as the merges expect.
+    red_m[wave * kCols + col] = lt > 0.f ? ref : -INFINITY;
     red_l[wave * kCols + col] = lt;
   }
   if (col < group) {
