@@ -188,9 +188,31 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   // valid rows (full tiles before the last one, the last one up to the sequence end, none outside
   // [0, num_tiles): those read as zeros).
   const int64_t tile_bytes = static_cast<int64_t>(kBlockN) * my_ss * 2;
-  // One query block of kPpBlockM rows: its own tile range, pipeline and epilogue. Every wave has
-  // finished with the LDS ring and every tile load has landed when it returns.
-  auto process = [&](const int qb) {
+  // The wave's query rows of block qb, the B operand of K Q^T: lane (r, half) holds row
+  // qb kPpBlockM + 32 wave + r, dims 16 ks + 8 half .. + 7 (zeros past the sequence).
+  u32x4 qf[D / 16];
+  auto load_q = [&](int qb) {
+    const int r = qb * kPpBlockM + wave * kRowsPerWave + (lane & 31);
+    const bool ok = r < a.seqlen_q;
+    const uint16_t* src = qp + static_cast<int64_t>(ok ? r : 0) * a.q_ss + 8 * half;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) qf[ks] = ok ? load16(src + 16 * ks) : u32x4{0, 0, 0, 0};
+  };
+  // Uses the Q registers, so that the compiler's wait for their loads sits here (it does not see
+  // the tile loads, and would otherwise wait for every later one at the first use of Q).
+  auto consume_q = [&]() {
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) asm volatile("" : "+v"(qf[ks]));
+  };
+  // The rows of the block to run next are in flight: the block before it loaded them in its last
+  // MFMA period (P V only, so Q is no longer needed there), hiding their latency behind that
+  // period and the epilogue. Measured per wave, loading them in the block's own prologue waited
+  // 4,000-6,800 cycles (the second group's loads queue behind the first's).
+  bool q_loaded = false;
+  // One query block of kPpBlockM rows: its own tile range, pipeline and epilogue (and, when next_qb
+  // >= 0, the query rows of block next_qb). Every wave has finished with the LDS ring and every
+  // tile load has landed when it returns.
+  auto process = [&](const int qb, const int next_qb) {
     const int q0 = qb * kPpBlockM;
     const int row0 = q0 + wave * kRowsPerWave;
     const int my_row = row0 + (lane & 31);
@@ -210,17 +232,11 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
       mask_from = min(mask_from, x < 0 ? 0 : x / kBlockN + 1);
     }
 
-    u32x4 qf[D / 16];
-    {
-      const bool ok = my_row < a.seqlen_q;
-      const uint16_t* src = qp + static_cast<int64_t>(ok ? my_row : 0) * a.q_ss + 8 * half;
-#pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks) qf[ks] = ok ? load16(src + 16 * ks) : u32x4{0, 0, 0, 0};
-      // Consume the Q registers here so the compiler's wait for them sits before the tile loads
-      // (it does not see those, and would otherwise wait for all of them at the first use of Q).
-#pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks) asm volatile("" : "+v"(qf[ks]));
+    if (!q_loaded) {
+      load_q(qb);
+      consume_q();
     }
+    q_loaded = false;
 
     const int last_rows = num_tiles > 0 ? min(kBlockN, a.seqlen_k - (num_tiles - 1) * kBlockN) : 1;
     const uint32_t full_bytes = static_cast<uint32_t>(((kBlockN - 1) * my_ss + D) * 2);
@@ -492,6 +508,12 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
             mfma_phase(slot, std::bool_constant<kDoPv>{}, std::bool_constant<kDoQk>{}, hook);
           }
         };
+        if constexpr (kMode == kLastT::value) {
+          if (next_qb >= 0) {
+            load_q(next_qb);
+            q_loaded = true;
+          }
+        }
         if constexpr (kGroup == 0) {
           if constexpr (kMode == kFirstT::value) prefetch_qk(slot);
           mfma();
@@ -539,6 +561,7 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     // Loads past the end may still be in flight into free slots: each wave waits for its own here,
     // and the barrier below for the others', before the ring is reused.
     wait_vmcnt<0>();
+    if (q_loaded) consume_q();
 
     const float lt = sum_halves(l);
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
@@ -591,7 +614,7 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     // The next block's prologue refills the ring, which the epilogue's staging reads just used (no
     // memory fence: the output stores need not complete first).
     if (i > 0) phase_barrier();
-    process(!a.causal ? item : i == 0 ? heavy : item);
+    process(!a.causal ? item : i == 0 ? heavy : item, i + 1 < blocks_here ? item : -1);
   }
 }
 
