@@ -533,7 +533,8 @@ def parse_args(argv=None):
         "--only",
         help="comma list of workloads to run: prefill, prefill_causal, decode (all of them), "
         f"{', '.join(DECODE)}, e2e_L, copy (a 1 GiB device copy, the calibration of the traffic "
-        "counters); default: all but copy",
+        "counters), gemm (a dense bf16 hipBLASLt GEMM, the chip's sustained MFMA rate); default: "
+        "all but copy and gemm",
     )
     return parser.parse_args(argv)
 
@@ -547,7 +548,7 @@ def selected_workloads(only: str | None, e2e: bool = True) -> list[str]:
         item = item.strip()
         if item == "decode":
             names += list(DECODE)
-        elif item in everything or item in ("copy", "e2e_L"):
+        elif item in everything or item in ("copy", "gemm", "e2e_L"):
             names.append(item)
         else:
             raise SystemExit(f"unknown workload {item!r}")
@@ -565,6 +566,31 @@ def bench_copy(steps: int) -> dict:
     mean_ms = sum(times) / len(times)
     return {"status": "ok", "bytes_read": FLUSH_BYTES, "bytes_written": FLUSH_BYTES,
             "mean_ms": mean_ms, "gbps_read_plus_write": 2 * FLUSH_BYTES / (mean_ms / 1e3) / 1e9}
+
+
+def bench_gemm(steps: int) -> dict:
+    """A dense bf16 GEMM through torch.matmul (hipBLASLt), 8192^3 = 2^40 FLOP like the prefill
+    launch, on iid N(0,1) operands and again on zeros: the MFMA rate the chip sustains under its
+    power limit with a vendor kernel, the context of the prefill kernel's fraction of peak (MFMA
+    power depends on the operands' bits, so the two rates differ)."""
+    import torch
+
+    n = 8192
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    a = torch.randn(n, n, device="cuda", dtype=torch.bfloat16, generator=gen)
+    b = torch.randn(n, n, device="cuda", dtype=torch.bfloat16, generator=gen)
+    c = torch.empty(n, n, device="cuda", dtype=torch.bfloat16)
+    flops = 2.0 * n ** 3
+    out = {"status": "ok", "shape": [n, n, n], "flops": flops, "via": "torch.matmul (hipBLASLt)"}
+    for label in ("randn", "zeros"):
+        if label == "zeros":
+            a.zero_()
+            b.zero_()
+        times, _ = time_op(lambda: torch.matmul(a, b, out=c), steps, 5, label=f"gemm_{label}")
+        ms = summarize(times)
+        out[label] = {"ms": ms, "tflops": flops / ms["median"] / 1e9,
+                      "frac_of_peak": flops / ms["median"] / 1e9 / PEAK_BF16_TFLOPS}
+    return out
 
 
 def overall_status(headline: dict | None, secondary: dict) -> int:
@@ -634,6 +660,9 @@ def main(argv=None) -> int:
     if "copy" in workloads:
         secondary["copy"] = bench_copy(args.steps)
         print(f"# copy: {json.dumps(secondary['copy'])}", file=sys.stderr, flush=True)
+    if "gemm" in workloads:
+        secondary["gemm"] = guarded("gemm", lambda: bench_gemm(args.steps))
+        print(f"# gemm: {json.dumps(secondary['gemm'])}", file=sys.stderr, flush=True)
     if "e2e_L" in workloads:
         secondary["e2e_L"] = guarded("e2e_L", lambda: bench_e2e_l(args.e2e_budget_s))
         print(f"# e2e_L: {json.dumps(secondary['e2e_L'])}", file=sys.stderr, flush=True)
