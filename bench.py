@@ -533,8 +533,8 @@ def parse_args(argv=None):
         "--only",
         help="comma list of workloads to run: prefill, prefill_causal, decode (all of them), "
         f"{', '.join(DECODE)}, e2e_L, copy (a 1 GiB device copy, the calibration of the traffic "
-        "counters), gemm (a dense bf16 hipBLASLt GEMM, the chip's sustained MFMA rate); default: "
-        "all but copy and gemm",
+        "counters), gemm (a dense bf16 hipBLASLt GEMM), mfma (register-only MFMA chains: the "
+        "matrix pipes' rate under the power limit); default: all but copy, gemm and mfma",
     )
     return parser.parse_args(argv)
 
@@ -548,7 +548,7 @@ def selected_workloads(only: str | None, e2e: bool = True) -> list[str]:
         item = item.strip()
         if item == "decode":
             names += list(DECODE)
-        elif item in everything or item in ("copy", "gemm", "e2e_L"):
+        elif item in everything or item in ("copy", "gemm", "mfma", "e2e_L"):
             names.append(item)
         else:
             raise SystemExit(f"unknown workload {item!r}")
@@ -591,6 +591,33 @@ def bench_gemm(steps: int) -> dict:
         out[label] = {"ms": ms, "tflops": flops / ms["median"] / 1e9,
                       "frac_of_peak": flops / ms["median"] / 1e9 / PEAK_BF16_TFLOPS}
     return out
+
+
+def bench_mfma_rate(steps: int) -> dict:
+    """The library's matrix-pipe rate probe (fl_mfma_rate_probe): 2,048 workgroups of register-only
+    v_mfma_f32_32x32x16_bf16 chains, no memory traffic, on pseudo-random operands shaped like
+    N(0,1) draws and on zeros. The MFMA rate the board's power limit leaves on random data, before
+    any softmax, LDS or HBM work: the ceiling the prefill kernel is held under."""
+    import torch
+    from flash_lab import _hip
+
+    workgroups, iters = 2048, 2500
+    out = torch.empty(workgroups * 256, device="cuda")
+    flops = float(workgroups) * 4 * iters * 16 * 32768
+
+    def run(zero):
+        stream = torch.cuda.current_stream().cuda_stream
+        if _hip.LIB.fl_mfma_rate_probe(out.data_ptr(), workgroups, iters, zero, stream) != 0:
+            raise RuntimeError(_hip.LIB.fl_last_error().decode())
+
+    result = {"status": "ok", "workgroups": workgroups, "iters": iters, "flops": flops,
+              "instruction": "v_mfma_f32_32x32x16_bf16"}
+    for label, zero in (("random", 0), ("zeros", 1)):
+        times, _ = time_op(lambda: run(zero), steps, 5, label=f"mfma_{label}")
+        ms = summarize(times)
+        result[label] = {"ms": ms, "tflops": flops / ms["median"] / 1e9,
+                         "frac_of_peak": flops / ms["median"] / 1e9 / PEAK_BF16_TFLOPS}
+    return result
 
 
 def overall_status(headline: dict | None, secondary: dict) -> int:
@@ -660,6 +687,9 @@ def main(argv=None) -> int:
     if "copy" in workloads:
         secondary["copy"] = bench_copy(args.steps)
         print(f"# copy: {json.dumps(secondary['copy'])}", file=sys.stderr, flush=True)
+    if "mfma" in workloads:
+        secondary["mfma"] = guarded("mfma", lambda: bench_mfma_rate(args.steps))
+        print(f"# mfma: {json.dumps(secondary['mfma'])}", file=sys.stderr, flush=True)
     if "gemm" in workloads:
         secondary["gemm"] = guarded("gemm", lambda: bench_gemm(args.steps))
         print(f"# gemm: {json.dumps(secondary['gemm'])}", file=sys.stderr, flush=True)

@@ -1,5 +1,7 @@
 // Toolchain check kernel: out = alpha * x + y (the reference's smoke_axpy op,
 // csrc/common/smoke.cu:12-45). It proves the gfx950 code object loads and runs on a new box.
+// Also the matrix-pipe rate probe, a calibration kernel with no counterpart in the reference.
+#include "gfx950.hpp"
 #include "launch.hpp"
 
 namespace fl {
@@ -12,7 +14,68 @@ __global__ void __launch_bounds__(256) axpy_kernel(const float* __restrict__ x,
   if (i < n) out[i] = alpha * x[i] + y[i];
 }
 
+// 16 pseudo-random bf16 values shaped like N(0,1) draws (random sign and mantissa, exponent
+// 2^-3 .. 2^1), or zeros: one MFMA operand register.
+__device__ __forceinline__ u32x4 probe_operand(uint32_t seed, bool zero) {
+  u32x4 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t x = seed * 8u + 2u * i + h;
+      x ^= x >> 16;
+      x *= 0x7feb352du;
+      x ^= x >> 15;
+      x *= 0x846ca68bu;
+      x ^= x >> 16;
+      const uint32_t bits = ((x >> 31) << 15) | ((124u + (x >> 8) % 5u) << 7) | (x & 0x7fu);
+      word |= bits << (16 * h);
+    }
+    v[i] = zero ? 0u : word;
+  }
+  return v;
+}
+
+// Register-only chains of v_mfma_f32_32x32x16_bf16: each wave issues 16 MFMAs per iteration on
+// four accumulators, cycling through four A and four B operand registers, with no memory traffic,
+// LDS or VALU work beside them. The matrix pipes' sustained rate under the board's power limit,
+// which depends on the operands' bits (random vs zero).
+__global__ void __launch_bounds__(256) mfma_rate_kernel(float* __restrict__ out, int iters,
+                                                        int zero) {
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  u32x4 a[4], b[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    a[i] = probe_operand(t * 16u + i, zero != 0);
+    b[i] = probe_operand(t * 16u + 8u + i, zero != 0);
+  }
+  f32x16 c[4] = {};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        c[i] = Elem<bf16_tag>::mfma32(a[(i + j) & 3], b[(i + 2 * j) & 3], c[i]);
+      }
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s += c[i][e];
+  }
+  out[t] = s;
+}
+
 }  // namespace
+
+hipError_t launch_mfma_rate(float* out, int workgroups, int iters, bool zero, hipStream_t stream) {
+  hipLaunchKernelGGL(mfma_rate_kernel, dim3(workgroups), dim3(256), 0, stream, out, iters,
+                     zero ? 1 : 0);
+  return hipGetLastError();
+}
 
 hipError_t launch_axpy(const float* x, const float* y, float alpha, float* out, int64_t n,
                        hipStream_t stream) {

@@ -137,6 +137,10 @@ SIGNATURES = {
             ctypes.c_void_p,
         ],
     ),
+    "fl_mfma_rate_probe": (
+        ctypes.c_int,
+        [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p],
+    ),
     "fl_set_knob": (ctypes.c_int, [ctypes.c_int32, ctypes.c_int64]),
     "fl_get_knob": (ctypes.c_int64, [ctypes.c_int32]),
     "fl_last_error": (ctypes.c_char_p, []),

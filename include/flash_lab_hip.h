@@ -166,6 +166,18 @@ int fl_mfma_tile_test(const void* a, const void* b, float* c, int32_t k, int32_t
                       fl_stream_t stream);
 
 /*
+ * Matrix-pipe rate probe. No counterpart in the reference: a calibration
+ * kernel for the prefill roofline. `workgroups` workgroups of 4 waves each run
+ * `iters` iterations of 16 v_mfma_f32_32x32x16_bf16 on register operands
+ * (pseudo-random bf16 shaped like N(0,1) draws, or zeros when zero_operands
+ * != 0), with no memory traffic beside one float per thread written to `out`
+ * (workgroups * 256 floats). FLOP per call: workgroups * 4 * iters * 16 *
+ * 32768. workgroups in [1, 65536], iters in [1, 2^20].
+ */
+int fl_mfma_rate_probe(float* out, int32_t workgroups, int32_t iters, int32_t zero_operands,
+                       fl_stream_t stream);
+
+/*
  * Routing overrides. No counterpart in the reference (its kernel choice is
  * fixed at build time): a test and experiment hook that pins a call to one
  * of this library's kernels, so the parity tests can run every shape on

@@ -251,6 +251,15 @@ def test_tile_test_rejects_bad_k():
     assert "K in {16, 32, 64}" in _hip.LIB.fl_last_error().decode()
 
 
+def test_rate_probe_rejects_bad_arguments():
+    assert _hip.LIB.fl_mfma_rate_probe(256, 0, 10, 0, None) != 0
+    assert "workgroups" in _hip.LIB.fl_last_error().decode()
+    assert _hip.LIB.fl_mfma_rate_probe(256, 8, 0, 0, None) != 0
+    assert "iters" in _hip.LIB.fl_last_error().decode()
+    assert _hip.LIB.fl_mfma_rate_probe(None, 8, 10, 0, None) != 0
+    assert "null" in _hip.LIB.fl_last_error().decode()
+
+
 def test_noalloc_decode_rejects_workspaces_beyond_its_scratch_array():
     # fl_decode_noalloc keeps the split partials in a 16 MiB array of its own; a call that would
     # need more is refused on the host, before any device call (so this runs without a GPU).

@@ -43,3 +43,21 @@ def test_key_order_over_64_keys(flash_ops):
     a[torch.arange(16), keys] = 1
     b = (torch.arange(64 * 16, dtype=torch.float32) % 251).view(64, 16).to(torch.bfloat16).cuda()
     torch.testing.assert_close(flash_ops.mma_tile_test(a, b, True), b.float()[keys])
+
+
+def test_rate_probe_runs(flash_ops):
+    # The calibration kernel behind bench.py's `mfma` leg: zero operands give exact zeros, random
+    # ones finite sums, the same on every call.
+    from flash_lab import _hip
+
+    out = torch.full((8 * 256,), float("nan"), device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    assert _hip.LIB.fl_mfma_rate_probe(out.data_ptr(), 8, 3, 1, stream) == 0
+    torch.cuda.synchronize()
+    assert (out == 0).all()
+    assert _hip.LIB.fl_mfma_rate_probe(out.data_ptr(), 8, 3, 0, stream) == 0
+    first = out.clone()
+    assert _hip.LIB.fl_mfma_rate_probe(out.data_ptr(), 8, 3, 0, stream) == 0
+    torch.cuda.synchronize()
+    assert torch.isfinite(first).all() and (first != 0).any()
+    assert torch.equal(first, out)
