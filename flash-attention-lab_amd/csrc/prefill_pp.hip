@@ -467,14 +467,11 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     //  * last (m = G): P V of tile G - 1 only, its slot G % kStages a run-time value;
     //  * loads only, m = G + 1 .. num_tiles: the group's tile loads and waits (the other group may
     //    still read those tiles) but no MFMAs,
-    // where G is the number of tiles any row of the group sees: num_tiles, or fewer for the group of
-    // earlier rows on a causal diagonal, whose tiles past those rows' diagonal it skips. Both groups
-    // run num_tiles + 1 periods of one barrier each.
-    int group_tiles = num_tiles;
-    if (a.causal) {
-      const int last = q0 + (group + 1) * kLoadWaves * kRowsPerWave - 1 + a.causal_offset;
-      group_tiles = last < 0 ? 0 : min(num_tiles, last / kBlockN + 1);
-    }
+    // where G is the number of tiles any row of the wave sees (my_tiles): num_tiles, or fewer for a
+    // wave of earlier rows on a causal diagonal, whose tiles past those rows' diagonal it skips. The
+    // waves of a group keep their turns on the MFMA pipes whatever their own G, and every wave runs
+    // num_tiles + 1 periods of one barrier each.
+    const int group_tiles = my_tiles;
     using kFirstT = std::integral_constant<int, 0>;
     using kFullT = std::integral_constant<int, 1>;
     using kLastT = std::integral_constant<int, 2>;
