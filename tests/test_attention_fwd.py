@@ -33,6 +33,7 @@ SHAPES = [
     (2, 1024, 1024, 4, 4, 128),
     (2, 37, 101, 4, 2, 64),  # S_q < S_k
     (1, 101, 37, 4, 4, 128),  # S_q > S_k: causal rows without keys
+    (1, 700, 300, 2, 1, 128),  # S_q > S_k over three blocks: a block, and waves, with no keys
     (2, 1, 300, 8, 2, 128),
 ]
 SLOW_SHAPES = [(1, 4096, 4096, 4, 4, 128), (1, 8192, 8192, 2, 1, 64)]
