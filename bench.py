@@ -594,26 +594,29 @@ def bench_gemm(steps: int) -> dict:
 
 
 def bench_mfma_rate(steps: int) -> dict:
-    """The library's matrix-pipe rate probe (fl_mfma_rate_probe): 2,048 workgroups of register-only
-    v_mfma_f32_32x32x16_bf16 chains, no memory traffic, on pseudo-random operands shaped like
-    N(0,1) draws and on zeros. The MFMA rate the board's power limit leaves on random data, before
-    any softmax, LDS or HBM work: the ceiling the prefill kernel is held under."""
+    """The library's matrix-pipe rate probe (fl_mfma_rate_probe): one workgroup of 8 waves per CU
+    running v_mfma_f32_32x32x16_bf16 chains with nothing else beside them, on pseudo-random
+    operands shaped like N(0,1) draws, on zeros, and on random operands whose A side is read from
+    LDS for every MFMA (the prefill kernel's fragment traffic, 1 KiB per wave per MFMA). The MFMA
+    rate the board's power limit leaves on random data, before and with the LDS traffic: the
+    ceiling the prefill kernel is held under."""
     import torch
     from flash_lab import _hip
 
-    workgroups, iters = 2048, 2500
-    out = torch.empty(workgroups * 256, device="cuda")
-    flops = float(workgroups) * 4 * iters * 16 * 32768
+    workgroups, iters = 256, 6000
+    out = torch.empty(workgroups * 512, device="cuda")
+    flops = float(workgroups) * 8 * iters * 16 * 32768
 
-    def run(zero):
+    def run(flags):
         stream = torch.cuda.current_stream().cuda_stream
-        if _hip.LIB.fl_mfma_rate_probe(out.data_ptr(), workgroups, iters, zero, stream) != 0:
+        if _hip.LIB.fl_mfma_rate_probe(out.data_ptr(), workgroups, iters, flags, stream) != 0:
             raise RuntimeError(_hip.LIB.fl_last_error().decode())
 
-    result = {"status": "ok", "workgroups": workgroups, "iters": iters, "flops": flops,
-              "instruction": "v_mfma_f32_32x32x16_bf16"}
-    for label, zero in (("random", 0), ("zeros", 1)):
-        times, _ = time_op(lambda: run(zero), steps, 5, label=f"mfma_{label}")
+    result = {"status": "ok", "workgroups": workgroups, "waves_per_workgroup": 8, "iters": iters,
+              "flops": flops, "instruction": "v_mfma_f32_32x32x16_bf16"}
+    for label, flags in (("random", 0), ("zeros", _hip.PROBE_ZERO_OPERANDS),
+                         ("random_lds_a", _hip.PROBE_LDS_A)):
+        times, _ = time_op(lambda: run(flags), steps, 5, label=f"mfma_{label}")
         ms = summarize(times)
         result[label] = {"ms": ms, "tflops": flops / ms["median"] / 1e9,
                          "frac_of_peak": flops / ms["median"] / 1e9 / PEAK_BF16_TFLOPS}

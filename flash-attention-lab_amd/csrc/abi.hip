@@ -495,12 +495,16 @@ int fl_mfma_tile_test(const void* a, const void* b, float* c, int32_t k, int32_t
   return FL_OK;
 }
 
-int fl_mfma_rate_probe(float* out, int32_t workgroups, int32_t iters, int32_t zero_operands,
+int fl_mfma_rate_probe(float* out, int32_t workgroups, int32_t iters, int32_t flags,
                        fl_stream_t stream) {
   if (workgroups < 1 || workgroups > 65536) return fail(FL_ERR_INVALID, "workgroups must be in [1, 65536]");
   if (iters < 1 || iters > (1 << 20)) return fail(FL_ERR_INVALID, "iters must be in [1, 2^20]");
+  if (flags < 0 || flags > (FL_PROBE_ZERO_OPERANDS | FL_PROBE_LDS_A))
+    return fail(FL_ERR_INVALID, "unknown probe flags");
   if (!out) return fail(FL_ERR_INVALID, "null output pointer");
-  const hipError_t err = fl::launch_mfma_rate(out, workgroups, iters, zero_operands != 0,
+  const hipError_t err = fl::launch_mfma_rate(out, workgroups, iters,
+                                              (flags & FL_PROBE_ZERO_OPERANDS) != 0,
+                                              (flags & FL_PROBE_LDS_A) != 0,
                                               static_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail(FL_ERR_LAUNCH, std::string("rate probe launch: ") + hipGetErrorString(err));
   return FL_OK;

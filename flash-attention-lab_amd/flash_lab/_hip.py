@@ -99,6 +99,10 @@ class DecodeParams(ctypes.Structure):
     ]
 
 
+# fl_mfma_rate_probe flags (include/flash_lab_hip.h).
+PROBE_ZERO_OPERANDS = 1
+PROBE_LDS_A = 2
+
 # Every symbol include/flash_lab_hip.h declares, with its ctypes signature.
 SIGNATURES = {
     "fl_attention_fwd": (ctypes.c_int, [ctypes.POINTER(AttnParams), ctypes.c_void_p]),

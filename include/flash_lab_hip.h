@@ -167,14 +167,20 @@ int fl_mfma_tile_test(const void* a, const void* b, float* c, int32_t k, int32_t
 
 /*
  * Matrix-pipe rate probe. No counterpart in the reference: a calibration
- * kernel for the prefill roofline. `workgroups` workgroups of 4 waves each run
- * `iters` iterations of 16 v_mfma_f32_32x32x16_bf16 on register operands
- * (pseudo-random bf16 shaped like N(0,1) draws, or zeros when zero_operands
- * != 0), with no memory traffic beside one float per thread written to `out`
- * (workgroups * 256 floats). FLOP per call: workgroups * 4 * iters * 16 *
- * 32768. workgroups in [1, 65536], iters in [1, 2^20].
+ * kernel for the prefill roofline. `workgroups` workgroups of 8 waves (two per
+ * SIMD, one workgroup per CU) each run `iters` iterations of 16
+ * v_mfma_f32_32x32x16_bf16 per wave. B operands come from registers; A
+ * operands from registers, or with FL_PROBE_LDS_A from an LDS read per MFMA
+ * (1 KiB per wave per MFMA, the prefill kernel's fragment traffic). Operands
+ * are pseudo-random bf16 shaped like N(0,1) draws, or zeros with
+ * FL_PROBE_ZERO_OPERANDS. Nothing else runs beside the MFMAs; one float per
+ * thread is written to `out` (workgroups * 512 floats). FLOP per call:
+ * workgroups * 8 * iters * 16 * 32768. workgroups in [1, 65536], iters in
+ * [1, 2^20].
  */
-int fl_mfma_rate_probe(float* out, int32_t workgroups, int32_t iters, int32_t zero_operands,
+#define FL_PROBE_ZERO_OPERANDS 1
+#define FL_PROBE_LDS_A 2
+int fl_mfma_rate_probe(float* out, int32_t workgroups, int32_t iters, int32_t flags,
                        fl_stream_t stream);
 
 /*

@@ -256,6 +256,8 @@ def test_rate_probe_rejects_bad_arguments():
     assert "workgroups" in _hip.LIB.fl_last_error().decode()
     assert _hip.LIB.fl_mfma_rate_probe(256, 8, 0, 0, None) != 0
     assert "iters" in _hip.LIB.fl_last_error().decode()
+    assert _hip.LIB.fl_mfma_rate_probe(256, 8, 10, 4, None) != 0
+    assert "flags" in _hip.LIB.fl_last_error().decode()
     assert _hip.LIB.fl_mfma_rate_probe(None, 8, 10, 0, None) != 0
     assert "null" in _hip.LIB.fl_last_error().decode()
 

@@ -45,19 +45,21 @@ def test_key_order_over_64_keys(flash_ops):
     torch.testing.assert_close(flash_ops.mma_tile_test(a, b, True), b.float()[keys])
 
 
-def test_rate_probe_runs(flash_ops):
+@pytest.mark.parametrize("lds_a", [False, True], ids=["registers", "lds"])
+def test_rate_probe_runs(flash_ops, lds_a):
     # The calibration kernel behind bench.py's `mfma` leg: zero operands give exact zeros, random
     # ones finite sums, the same on every call.
     from flash_lab import _hip
 
-    out = torch.full((8 * 256,), float("nan"), device="cuda")
+    flags = _hip.PROBE_LDS_A if lds_a else 0
+    out = torch.full((8 * 512,), float("nan"), device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
-    assert _hip.LIB.fl_mfma_rate_probe(out.data_ptr(), 8, 3, 1, stream) == 0
+    assert _hip.LIB.fl_mfma_rate_probe(out.data_ptr(), 8, 3, flags | _hip.PROBE_ZERO_OPERANDS, stream) == 0
     torch.cuda.synchronize()
     assert (out == 0).all()
-    assert _hip.LIB.fl_mfma_rate_probe(out.data_ptr(), 8, 3, 0, stream) == 0
+    assert _hip.LIB.fl_mfma_rate_probe(out.data_ptr(), 8, 3, flags, stream) == 0
     first = out.clone()
-    assert _hip.LIB.fl_mfma_rate_probe(out.data_ptr(), 8, 3, 0, stream) == 0
+    assert _hip.LIB.fl_mfma_rate_probe(out.data_ptr(), 8, 3, flags, stream) == 0
     torch.cuda.synchronize()
     assert torch.isfinite(first).all() and (first != 0).any()
     assert torch.equal(first, out)
