@@ -388,13 +388,9 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     // the max / rescale path and recompute them. A row without a reference yet (kNoRef) overflows
     // on its first tile with a visible key. The row max is therefore not needed on most tiles, and
     // every probability stays <= kSumLimit.
+    // It runs only for tiles t < my_tiles: a wave's periods past its last visible tile are
+    // loads-only.
     auto softmax_body = [&](int t) {
-      if (static_cast<unsigned>(t) >= static_cast<unsigned>(my_tiles)) {
-        // This wave sees no key of tile t: the P V that follows must add nothing.
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pf[i] = u32x4{0, 0, 0, 0};
-        return;
-      }
       if (t >= mask_from) {
         asm volatile("" ::: "memory");
         // acc_key(j, half) = acc_key(j, 0) + 4 half: fold the lane's part into the limit so every
@@ -471,7 +467,7 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     // wave of earlier rows on a causal diagonal, whose tiles past those rows' diagonal it skips. The
     // waves of a group keep their turns on the MFMA pipes whatever their own G, and every wave runs
     // num_tiles + 1 periods of one barrier each.
-    const int group_tiles = my_tiles;
+    const int wave_tiles = my_tiles;
     using kFirstT = std::integral_constant<int, 0>;
     using kFullT = std::integral_constant<int, 1>;
     using kLastT = std::integral_constant<int, 2>;
@@ -535,14 +531,14 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
       };
       if (num_tiles == 0) return;  // no key at all: nothing to multiply
       int m = 0;
-      if (group_tiles > 0) {
+      if (wave_tiles > 0) {
         period(0, 0, kFirstT{});
-        for (m = 1; m < group_tiles;) {
+        for (m = 1; m < wave_tiles;) {
           bool done = false;
           static_for<0, kStages>([&](auto j) {
             if (done) return;
             period(m, (1 + decltype(j)::value) % kStages, kFullT{});
-            done = ++m == group_tiles;
+            done = ++m == wave_tiles;
           });
         }
         period(m, m % kStages, kLastT{});
