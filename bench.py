@@ -49,7 +49,7 @@ for _p in (REPO, REPO / "flash-attention-lab_amd"):
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
 FLUSH_BYTES = 1 << 30  # larger than the 256 MB Infinity Cache
-BASELINE_TFLOPS = 229.2  # reference mma_pipelined, non-causal, H100
+BASELINE_TFLOPS = 229.2  # reference mma_pipelined, non-causal, H100 SXM5 (reference bench/results/h100-80gb-hbm3/summary-cc64b18.md:154)
 
 PREFILL = dict(batch=4, heads=32, heads_kv=32, seqlen=4096, head_dim=128)
 DECODE = {
@@ -754,7 +754,7 @@ def main(argv=None) -> int:
         "scaling": "weak",
         "vs_baseline": value / BASELINE_TFLOPS if value else None,
         "baseline": {"value": BASELINE_TFLOPS, "unit": "TFLOP/s",
-                     "what": "reference mma_pipelined, non-causal, H100 SXM5 (BASELINE.md)"},
+                     "what": "reference mma_pipelined, non-causal, H100 SXM5 (reference bench/results/h100-80gb-hbm3/summary-cc64b18.md:154)"},
         "dtype": "bf16",
         "data": "synthetic iid N(0,1), torch.Generator seed 0",
         "config": {
