@@ -400,8 +400,12 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
         for (int j = 0; j < 16; ++j) {
           constexpr int kBase = 0;
           const int kj = acc_key(j, kBase);
-          if (kj > lim) s0[j] = -INFINITY;
-          if (kj + 32 > lim) s1[j] = -INFINITY;
+          s0[j] = kj > lim ? -INFINITY : s0[j];
+          s1[j] = kj + 32 > lim ? -INFINITY : s1[j];
+          // One compare and one select per score: left free, the scheduler kept all 32 compare
+          // results live in scalar register pairs and chained them, which made the kernel spill
+          // 86 scalar registers (reloaded on every masked tile).
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
       float rs = probabilities(-ref);
