@@ -7,10 +7,11 @@
 // with the -inf-safe reference point, bottom-right causal mask, 1/l epilogue) follows the
 // reference's definitions (csrc/prefill/mma_tile.cuh:60-174, flash_lab/reference.py:90-152).
 //
-// Why: within one wave, VALU instructions issued between MFMAs do not overlap with them (on gfx950
-// an MFMA followed by 8 independent FMAs takes as long as the two back to back), while an MFMA
-// stream in one wave and a VALU stream in another wave of the same SIMD run concurrently at full
-// MFMA rate. A wave issues at most one instruction every 4-5 cycles whatever its kind, so the
+// Why: within one wave, VALU instructions issued between MFMAs overlap with them only in part (on
+// gfx950, 8 independent FMAs after each MFMA made a register-only loop 1.3x slower, and the
+// exponential-heavy softmax, which also waits for its scores, overlaps less), while an MFMA stream
+// in one wave and a VALU stream in another wave of the same SIMD run concurrently at full MFMA
+// rate. A wave issues at most one instruction every 4-5 cycles whatever its kind, so the
 // softmax wave's phase costs about 5 cycles per instruction (about 9.6 per exponential) and must
 // stay below the MFMA phase's 1024 cycles: everything that is not softmax arithmetic (tile loads,
 // their descriptors) is issued by the MFMA wave, which has idle issue slots while its MFMAs run.
