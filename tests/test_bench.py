@@ -33,6 +33,9 @@ def test_workload_selection():
     assert bench.selected_workloads(None, e2e=False) == ["prefill", "prefill_causal", *bench.DECODE]
     assert bench.selected_workloads("decode,copy") == [*bench.DECODE, "copy"]
     assert bench.selected_workloads("e2e_L", e2e=False) == ["e2e_L"]
+    # The calibration legs (hipBLASLt GEMM, MFMA rate probe) run only when asked for.
+    assert bench.selected_workloads("mfma,gemm,prefill") == ["mfma", "gemm", "prefill"]
+    assert "mfma" not in bench.selected_workloads(None) and "gemm" not in bench.selected_workloads(None)
     with pytest.raises(SystemExit):
         bench.selected_workloads("nope")
 
