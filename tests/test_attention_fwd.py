@@ -121,6 +121,18 @@ def test_headline_shape_sampled_rows(causal):
     check_prefill(out, lse, q, k, v, causal, rows=sampled_rows(4096, 256))
 
 
+def test_paired_blocks_with_an_odd_block_count():
+    # Large non-causal grids run two consecutive query blocks per workgroup; with 17 blocks per
+    # (batch, head) the last workgroup of each runs one. 256 sampled rows of every (batch, head),
+    # the last block's rows included.
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    shape = (2, 4196, 32, 128)
+    q, k, v = (torch.randn(shape, device="cuda", dtype=torch.bfloat16, generator=gen) for _ in range(3))
+    out, lse = flash_lab.attention(q, k, v, causal=False, return_lse=True)
+    rows = torch.unique(torch.cat([sampled_rows(4196, 256), torch.arange(4096, 4196, 7)]))
+    check_prefill(out, lse, q, k, v, False, rows=rows)
+
+
 @pytest.mark.parametrize("impl,dtype", IMPLS, ids=lambda x: str(x).replace("torch.", ""))
 def test_large_scores(impl, dtype, route):
     # Scores of order 100 overflow exp() unless the running max is subtracted (on each kernel: the
