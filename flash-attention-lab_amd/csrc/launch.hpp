@@ -26,7 +26,6 @@ struct PrefillArgs {
   float scale;       // softmax scale, natural-log domain (used for the LSE)
   float scale_log2;  // scale * log2(e): probabilities are 2^(s * scale_log2 - ref)
   int q_blocks;      // ceil(S_q / rows per workgroup)
-  int pair_blocks;   // ping-pong kernel, non-causal: two consecutive query blocks per workgroup
 };
 
 // Decode problem. q [B, H, D], caches [B, S_max, H_kv, D], o [B, H, D], lse [B, H].

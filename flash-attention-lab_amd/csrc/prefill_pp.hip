@@ -52,7 +52,6 @@ constexpr int kPpThreads = 64 * kPpWaves;
 constexpr int kPpBlockM = kRowsPerWave * kPpWaves;  // 256 query rows per workgroup
 constexpr int kLoadWaves = 4;                       // waves per group: one group per tensor
 constexpr int kXcds = 8;
-constexpr int64_t kPairMinWorkgroups = 512;  // pair non-causal blocks from this paired grid size
 constexpr float kLn2 = 0.693147180559945309f;
 // Largest lane sum of probabilities (32 of them) kept without moving the reference point.
 constexpr float kSumLimit = 32768.f;
@@ -140,15 +139,12 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   const int group = wave >> 2;
   const int half = lane >> 5;
 
-  // Work item: (batch, head) and query blocks. Non-causal: one block per workgroup, or blocks 2i
-  // and 2i + 1 when the launch pairs them (grids large enough to fill the GPU twice over with
-  // pairs; the second block's query rows are then loaded in the first block's last period).
-  // Causal: the blocks of a (batch, head) go in pairs (q_blocks - 1 - i, i), heavy first, so
-  // every workgroup runs about the same number of tiles (a plain heaviest-first order still
-  // leaves a tail of heavy blocks dealt late) and the light block's K and V are a prefix of the
-  // heavy one's.
+  // Work item: (batch, head) and query blocks. Non-causal: one block per workgroup. Causal: the
+  // blocks of a (batch, head) go in pairs (q_blocks - 1 - i, i), heavy first, so every workgroup
+  // runs about the same number of tiles (a plain heaviest-first order still leaves a tail of heavy
+  // blocks dealt late) and the light block's K and V are a prefix of the heavy one's.
   const int work = xcd_remap(blockIdx.x, gridDim.x);
-  const int items_per_bh = a.causal || a.pair_blocks ? (a.q_blocks + 1) / 2 : a.q_blocks;
+  const int items_per_bh = a.causal ? (a.q_blocks + 1) / 2 : a.q_blocks;
   const int bh = work / items_per_bh;
   const int item = work - bh * items_per_bh;
   const int b = bh / a.heads;
@@ -610,35 +606,20 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   };
 
   // One call site (a loop), so the block body is inlined once.
-  int first = item;
-  int second = item;
-  int blocks_here = 1;
-  if (a.causal) {
-    first = a.q_blocks - 1 - item;
-    blocks_here = item < first ? 2 : 1;
-  } else if (a.pair_blocks) {
-    first = 2 * item;
-    second = first + 1;
-    blocks_here = second < a.q_blocks ? 2 : 1;
-  }
+  const int heavy = a.q_blocks - 1 - item;
+  const int blocks_here = a.causal && item < heavy ? 2 : 1;
   for (int i = 0; i < blocks_here; ++i) {
     // The next block's prologue refills the ring, which the epilogue's staging reads just used (no
     // memory fence: the output stores need not complete first).
     if (i > 0) phase_barrier();
-    process(i == 0 ? first : second, i + 1 < blocks_here ? second : -1);
+    process(!a.causal ? item : i == 0 ? heavy : item, i + 1 < blocks_here ? item : -1);
   }
 }
 
 template <typename Tag, int D>
 hipError_t launch_typed(PrefillArgs args, hipStream_t stream) {
   args.q_blocks = (args.seqlen_q + kPpBlockM - 1) / kPpBlockM;
-  // Non-causal pairs of blocks when the paired grid still fills MI355X's 256 CUs twice over:
-  // (4, 32, 32, 4096, 128) 1,267-1,278 -> 1,274-1,282 TFLOP/s on one box; smaller grids keep one
-  // block per workgroup, so that no CU idles for lack of work.
-  const int64_t pairs = static_cast<int64_t>((args.q_blocks + 1) / 2) * args.batch * args.heads;
-  args.pair_blocks = !args.causal && args.q_blocks > 1 && pairs >= kPairMinWorkgroups ? 1 : 0;
-  const int items_per_bh =
-      args.causal || args.pair_blocks ? (args.q_blocks + 1) / 2 : args.q_blocks;
+  const int items_per_bh = args.causal ? (args.q_blocks + 1) / 2 : args.q_blocks;
   const int blocks = items_per_bh * args.batch * args.heads;
   hipLaunchKernelGGL((prefill_pp_kernel<Tag, D>), dim3(blocks), dim3(kPpThreads), 0, stream, args);
   return hipGetLastError();

@@ -121,10 +121,10 @@ def test_headline_shape_sampled_rows(causal):
     check_prefill(out, lse, q, k, v, causal, rows=sampled_rows(4096, 256))
 
 
-def test_paired_blocks_with_an_odd_block_count():
-    # Large non-causal grids run two consecutive query blocks per workgroup; with 17 blocks per
-    # (batch, head) the last workgroup of each runs one. 256 sampled rows of every (batch, head),
-    # the last block's rows included.
+def test_ragged_long_sequence_sampled_rows():
+    # 4,196 rows: 16 full 256-row blocks and a ragged 17th per (batch, head), on a grid large
+    # enough for the ping-pong kernel. 256 sampled rows of every (batch, head), plus rows of the
+    # ragged block.
     gen = torch.Generator(device="cuda").manual_seed(5)
     shape = (2, 4196, 32, 128)
     q, k, v = (torch.randn(shape, device="cuda", dtype=torch.bfloat16, generator=gen) for _ in range(3))
