@@ -52,6 +52,8 @@ FLUSH_BYTES = 1 << 30  # larger than the 256 MB Infinity Cache
 BASELINE_TFLOPS = 229.2  # reference mma_pipelined, non-causal, H100 SXM5 (reference bench/results/h100-80gb-hbm3/summary-cc64b18.md:154)
 
 PREFILL = dict(batch=4, heads=32, heads_kv=32, seqlen=4096, head_dim=128)
+# head_dim 64 at the same tokens and half the FLOP (64 heads of 64): the kernel's D = 64 case.
+PREFILL_D64 = dict(batch=4, heads=64, heads_kv=64, seqlen=4096, head_dim=64)
 DECODE = {
     "B1-MHA": dict(batch=1, heads=32, heads_kv=32, context=32768, head_dim=128),
     "B8-MHA": dict(batch=8, heads=32, heads_kv=32, context=32768, head_dim=128),
@@ -107,6 +109,49 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def env_record() -> dict:
+    """What ran, in the spirit of the reference's bench/env.py:39-106: the checkout's git HEAD
+    (git is absent where the benchmark runs on a copied tree, so the library's build record, which
+    names the HEAD it was built from, stands beside it), the library's own hash and version,
+    torch, HIP, ROCm, Python, and the GPU's driver, VBIOS and power cap from amdsmi."""
+    import hashlib
+    import platform
+    import subprocess
+
+    import torch
+
+    from flash_lab import _hip
+    from flash_lab.observe import driver_record
+
+    rec: dict = {"python": platform.python_version(), "torch": torch.__version__,
+                 "hip": getattr(torch.version, "hip", None)}
+    try:
+        rec["rocm"] = Path("/opt/rocm/.info/version").read_text().strip()
+    except OSError:
+        rec["rocm"] = None
+    try:
+        proc = subprocess.run(["git", "-C", str(REPO), "rev-parse", "HEAD"], capture_output=True,
+                              text=True, timeout=10)
+        rec["git_head"] = proc.stdout.strip() if proc.returncode == 0 else None
+    except (OSError, subprocess.TimeoutExpired):
+        rec["git_head"] = None
+    lib_path = Path(_hip.LIB._name)
+    library = {"path": str(lib_path.relative_to(REPO)) if lib_path.is_relative_to(REPO) else str(lib_path),
+               "version": _hip.LIB.fl_version().decode()}
+    try:
+        library["sha256_16"] = hashlib.sha256(lib_path.read_bytes()).hexdigest()[:16]
+    except OSError:
+        pass
+    try:
+        library["build"] = json.loads(lib_path.with_suffix(".build.json").read_text())
+        library["build"].pop("flags", None)
+    except (OSError, ValueError):
+        library["build"] = None
+    rec["library"] = library
+    rec["gpu_driver"] = driver_record(torch.cuda.current_device())
+    return rec
+
+
 TRAFFIC_PROFILE = REPO / "profiles" / "prefill_pp_kernel_4x32x32x4096x128_bf16.md"
 
 
@@ -160,19 +205,23 @@ def check_prefill(out, qc, kc, vc, causal, rows) -> dict:
     import torch.nn.functional as F
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
-    from oracle import reference
+    from oracle import c_oracle
 
-    ref = reference.attention_rows(qc, kc, vc, rows, causal=causal)
+    # The oracle's C loops (pinned to its torch attention_rows at 1e-12 in tests/test_oracle.py):
+    # the same float64 rows in a fraction of the time.
+    ref, _ = c_oracle.attention_rows(qc, kc, vc, rows, causal=causal)
     err = (out.cpu()[:, rows].double() - ref).abs().max().item()
     mask = None
     if causal:
         cols = torch.arange(kc.shape[1])[None, :]
         mask = cols <= rows[:, None] + (kc.shape[1] - qc.shape[1])
+    group = qc.shape[2] // kc.shape[2]
+    kr, vr = (x.repeat_interleave(group, dim=2) if group > 1 else x for x in (kc, vc))
     with sdpa_kernel(SDPBackend.MATH):
         base = F.scaled_dot_product_attention(
             qc[:, rows].transpose(1, 2).contiguous(),
-            kc.transpose(1, 2).contiguous(),
-            vc.transpose(1, 2).contiguous(),
+            kr.transpose(1, 2).contiguous(),
+            vr.transpose(1, 2).contiguous(),
             attn_mask=mask,
         ).transpose(1, 2)
     err_torch = (base.double() - ref).nan_to_num(0.0).abs().max().item()
@@ -233,18 +282,63 @@ def time_op(run, steps: int, warmup: int, flush=None, label: str = "step") -> tu
     return [s.elapsed_time(e) for s, e in zip(starts, ends)], wall
 
 
+CLOCK_WINDOW_S = 1.0  # the GPU clock and power are sampled over this much of the same work
+
+
+def gpu_window(run, step_ms: float, flush=None, seconds: float = CLOCK_WINDOW_S) -> dict:
+    """Shader and memory clock, socket power and hotspot temperature of the GPU (amdsmi, through
+    flash_lab.observe.ClockSampler) while it runs the workload's step again for `seconds` (the
+    timed steps themselves are too short for the sampled metrics, which refresh every few
+    milliseconds at best), in the reference's form (bench/clocks.py:18-71, the
+    gpu_during_timing field of its result files): min / median / max per field. Launches go out
+    in batches of about 25 ms of work with at most two batches queued, and one sample is taken
+    after each batch, so every sample falls while the GPU is busy with this workload."""
+    import torch
+
+    from flash_lab.observe import ClockSampler
+
+    per_batch = max(1, int(25.0 / max(step_ms, 1e-3)))
+    with ClockSampler(interval_ms=0) as sampler:
+        if not sampler.available:
+            return {"available": False, "reason": "amdsmi cannot read this GPU"}
+        torch.cuda.synchronize()
+        start = time.time()
+        queued = []
+        steps = 0
+        while time.time() - start < seconds:
+            for _ in range(per_batch):
+                if flush is not None:
+                    flush.zero_()
+                run()
+            steps += per_batch
+            event = torch.cuda.Event()
+            event.record()
+            queued.append(event)
+            if len(queued) > 2:
+                queued.pop(0).synchronize()
+            sampler.sample()
+        torch.cuda.synchronize()
+        end = time.time()
+        window = sampler.window(start, end)
+    return {"available": window is not None, "window_s": end - start, "steps": steps,
+            **(window or {})}
+
+
 # ----------------------------------------------------------------------------------------------
 # The reference CPU path: the oracle (PyTorch fp64) on the host cores, timed with perf_counter.
 
 CPU_LEG_BUDGET_S = 6.0  # timed work per CPU leg, beyond its warmup
 CPU_MIN_REPS = 3
 CPU_MAX_REPS = 10
+CPU_DECODE_REPS = 10  # the decode legs always run this many (BASELINE.md: median of >= 10 runs)
 
 
-def time_cpu(fn, budget_s: float = CPU_LEG_BUDGET_S, warmed_up: bool = False) -> dict:
+def time_cpu(fn, budget_s: float = CPU_LEG_BUDGET_S, warmed_up: bool = False,
+             min_reps: int = CPU_MIN_REPS) -> dict:
     """perf_counter times (ms) of fn() on the host: 2 warmup runs (1 when a run takes over a
     second, none when the caller has just run the same computation), then runs until budget_s is
-    spent, at least CPU_MIN_REPS and at most CPU_MAX_REPS; median, p10, p90 and the counts."""
+    spent, at least min_reps and at most max(min_reps, CPU_MAX_REPS); median, p10, p90 and the
+    counts."""
     warmup = 0
     if not warmed_up:
         t0 = time.perf_counter()
@@ -255,8 +349,8 @@ def time_cpu(fn, budget_s: float = CPU_LEG_BUDGET_S, warmed_up: bool = False) ->
             warmup = 2
     times = []
     start = time.perf_counter()
-    while len(times) < CPU_MAX_REPS and (
-        len(times) < CPU_MIN_REPS or time.perf_counter() - start < budget_s
+    while len(times) < max(min_reps, CPU_MAX_REPS) and (
+        len(times) < min_reps or time.perf_counter() - start < budget_s
     ):
         t0 = time.perf_counter()
         fn()
@@ -311,42 +405,55 @@ def cpu_prefill_leg(qc, kc, vc, rows, causal) -> dict:
                       f"{b * h} (batch, head), {'causal' if causal else 'non-causal'}"}
 
 
-def cpu_decode_leg(qc, kc, vc, lens, kv_bytes) -> dict:
-    """The full fp64 decode (oracle decode: every sequence, every key) timed on the host, in GB/s
-    of the bf16 K+V bytes the GPU reads."""
+CPU_DECODE_SEQUENCES = 2  # sequences of a decode batch the CPU leg times (a bounded sample)
+
+
+def cpu_decode_leg(qc, kc, vc, lens) -> dict:
+    """The fp64 decode of the oracle (every key of each sampled sequence) timed on the host, at
+    least CPU_DECODE_REPS times, in GB/s of the bf16 K+V bytes of the sequences it covers. Batches
+    of more than CPU_DECODE_SEQUENCES sequences are sampled (their first ones): the full B=8
+    decode takes about a second per run on the host, and the sample keeps the leg to seconds while
+    giving every figure ten or more runs."""
     from oracle import reference
 
-    t = time_cpu(lambda: reference.decode(qc, kc, vc, lens), warmed_up=True)
+    n = min(CPU_DECODE_SEQUENCES, qc.shape[0])
+    qs, ks, vs, ls = qc[:n], kc[:n], vc[:n], lens[:n]
+    t = time_cpu(lambda: reference.decode(qs, ks, vs, ls), min_reps=CPU_DECODE_REPS)
+    kv_bytes = 2.0 * int(ls.sum()) * kc.shape[2] * kc.shape[3] * kc.element_size()
     return {**t, "gbps": kv_bytes / (t["ms"]["median"] / 1e3) / 1e9,
-            "sample": f"oracle fp64 decode of all {qc.shape[0]} sequences x {kc.shape[1]} keys"}
+            "sample": f"oracle fp64 decode of {n} of {qc.shape[0]} sequences x {kc.shape[1]} keys "
+                      f"x {qc.shape[2]} heads ({kv_bytes:.4g} B of bf16 K+V)"}
 
 
 # ----------------------------------------------------------------------------------------------
 # GPU legs
 
 
-def bench_prefill(steps: int, warmup: int, causal: bool, cpu: bool) -> dict:
+def bench_prefill(steps: int, warmup: int, causal: bool, cpu: bool, cfg: dict = PREFILL,
+                  label: str | None = None, clocks: bool = True) -> dict:
     import torch
 
     import flash_lab
 
-    cfg = PREFILL
+    label = label or ("prefill_causal" if causal else "prefill")
     q, k, v = prefill_inputs(cfg)
     qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
     rows = sampled_rows(cfg["seqlen"], CHECK_ROWS)
     check = check_prefill(flash_lab.attention(q, k, v, causal=causal), qc, kc, vc, causal, rows)
     if not check["correct"]:
         return {"status": "incorrect", **check}
-    times, wall = time_op(lambda: flash_lab.attention(q, k, v, causal=causal), steps, warmup,
-                          label="prefill_causal" if causal else "prefill")
+    run = lambda: flash_lab.attention(q, k, v, causal=causal)  # noqa: E731
+    times, wall = time_op(run, steps, warmup, label=label)
     flops = attention_flops(cfg["batch"], cfg["heads"], cfg["seqlen"], cfg["seqlen"],
                             cfg["head_dim"], causal)
     mean_ms = sum(times) / len(times)
     stats = summarize(times)
+    gpu = gpu_window(run, stats["median"]) if clocks else None
     del q, k, v
     torch.cuda.empty_cache()
     result = {
         "status": "ok",
+        "config": {**cfg, "causal": causal},
         "causal": causal,
         "flops": flops,
         "ms": stats,
@@ -357,6 +464,8 @@ def bench_prefill(steps: int, warmup: int, causal: bool, cpu: bool) -> dict:
         "frac_of_peak": flops / (mean_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS,
         **check,
     }
+    if gpu is not None:
+        result["gpu_clocks"] = gpu
     if cpu:
         result["reference_cpu_path"] = cpu_prefill_leg(qc, kc, vc, rows, causal)
     return result
@@ -406,10 +515,14 @@ def bench_decode(name: str, steps: int, warmup: int, flush, cpu: bool) -> dict:
              "checked": f"all {b} sequences x {ctx} keys x {h} heads, all outputs finite"}
     if not ok:
         return {"status": "incorrect", **check}
-    times, _ = time_op(lambda: flash_lab.decode(q, k_used, v_used, seq_lens, block_tables=tables),
-                       steps, warmup, flush, label=name)
+    run = lambda: flash_lab.decode(q, k_used, v_used, seq_lens, block_tables=tables)  # noqa: E731
+    times, _ = time_op(run, steps, warmup, flush, label=name)
     stats = summarize(times)
     mean_ms = sum(times) / len(times)
+    # Sampled without the flush between steps (its memset would dominate the window); every
+    # benchmark cache here is larger than the 256 MB Infinity Cache, so the steps still stream
+    # from HBM.
+    gpu = gpu_window(run, stats["median"])
     kv = decode_kv_bytes(b, hkv, ctx, d, 2)
     splits, _ = _hip.decode_plan(b, h, hkv, d, ctx, torch.bfloat16,
                                  cu_count_=_hip.cu_count(torch.cuda.current_device()))
@@ -426,6 +539,7 @@ def bench_decode(name: str, steps: int, warmup: int, flush, cpu: bool) -> dict:
         "gbps": kv / (stats["median"] / 1e3) / 1e9,
         "gbps_mean": kv / (mean_ms / 1e3) / 1e9,
         "frac_of_peak": kv / (mean_ms / 1e3) / 1e9 / PEAK_HBM_GBPS,
+        "gpu_clocks": gpu,
         "roofline": {"bound": "hbm", "achieved": kv / (mean_ms / 1e3) / 1e9, "peak": PEAK_HBM_GBPS,
                      "unit": "GB/s", "frac": kv / (mean_ms / 1e3) / 1e9 / PEAK_HBM_GBPS,
                      "per_launch": f"{kv:.4g} B of K+V (every cached row once), mean {mean_ms:.4f} ms "
@@ -435,8 +549,110 @@ def bench_decode(name: str, steps: int, warmup: int, flush, cpu: bool) -> dict:
     # The reference CPU path for the three decode configurations BASELINE.json names (the paged
     # and 8-head variants are this repo's additions and have the same oracle work as B8-GQA).
     if cpu and name in ("B1-MHA", "B8-MHA", "B8-GQA"):
-        result["reference_cpu_path"] = cpu_decode_leg(qc, kc, vc, lc, kv)
+        result["reference_cpu_path"] = cpu_decode_leg(qc, kc, vc, lc)
     return result
+
+
+# ----------------------------------------------------------------------------------------------
+# --only sweep: the reference's other benchmark suites (bench/suites.py:63-125), each shape checked
+# and timed like the headline legs, beside the reference's H100 figure for the kernel this build
+# replaces (mma_pipelined for prefill, splitkv for decode). Sources, under the reference's
+# bench/results/h100-80gb-hbm3/: summary-cc64b18.md (medians of three runs) where the summary has
+# the suite, else the single run file named. The reference's decode GB/s count the q and o bytes
+# too (bench/flops.py:51-57); here they are compared against "gbps_with_q_o".
+SUMMARY = "summary-cc64b18.md"
+SWEEP_PREFILL = [
+    # (B, H, H_kv, S, D): (non-causal, causal) H100 TFLOP/s, source
+    ((4, 32, 32, 1024, 128), (219.3, 177.4), f"{SUMMARY}:140,147"),
+    ((4, 32, 32, 4096, 128), (229.2, 216.7), f"{SUMMARY}:154,161"),
+    ((2, 32, 32, 8192, 128), (230.8, 224.2), f"{SUMMARY}:168,175"),
+    ((1, 32, 32, 16384, 128), (228.1, 231.6), f"{SUMMARY}:182,189"),
+    ((8, 16, 16, 2048, 64), (200.2, 177.2), f"{SUMMARY}:196,203"),
+    ((4, 32, 8, 4096, 128), (227.4, 212.5), f"{SUMMARY}:210,217"),
+    ((32, 32, 32, 512, 128), (214.6, 170.3), "20261003-074548-ef88a7a-prefill_seqlen.json"),
+    ((16, 32, 32, 1024, 128), (207.6, 199.6), "20261003-074548-ef88a7a-prefill_seqlen.json"),
+    ((8, 32, 32, 2048, 128), (223.2, 211.5), "20261003-074548-ef88a7a-prefill_seqlen.json"),
+]
+_DECODE_CTX = {(1, 32, 512): (174.4, 40), (1, 32, 2048): (597.1, 46), (1, 32, 8192): (1679.9, 52),
+               (1, 32, 32768): (2171.0, 58), (1, 8, 512): (43.0, 64), (1, 8, 2048): (161.1, 70),
+               (1, 8, 8192): (521.9, 76), (1, 8, 32768): (674.2, 82), (8, 32, 512): (1102.4, 88),
+               (8, 32, 2048): (2100.0, 94), (8, 32, 8192): (2483.4, 100),
+               (8, 32, 32768): (2691.7, 106), (8, 8, 512): (322.2, 112), (8, 8, 2048): (652.5, 118),
+               (8, 8, 8192): (948.8, 124), (8, 8, 32768): (1135.0, 130)}
+SWEEP_DECODE = [
+    # (B, H, H_kv, context, D): H100 GB/s (K+V+q+o), source
+    *[((b, 32, hkv, ctx, 128), gbps, f"{SUMMARY}:{line}")
+      for (b, hkv, ctx), (gbps, line) in _DECODE_CTX.items()],
+    *[((b, 32, 8, 2048, 128), gbps, f"{SUMMARY}:{line}")
+      for b, gbps, line in ((4, 566.2, 17), (16, 904.5, 23), (64, 1096.4, 29))],
+    *[((b, 32, 8, ctx, 64), gbps, "20261003-074603-ef88a7a-decode_d64.json")
+      for (b, ctx), gbps in {(1, 2048): 84.9, (1, 8192): 292.2, (1, 32768): 603.3,
+                             (8, 2048): 581.3, (8, 8192): 884.2, (8, 32768): 1048.6}.items()],
+    *[((1, 32, hkv, ctx, 128), gbps, "20261003-074642-ef88a7a-decode_long.json")
+      for (hkv, ctx), gbps in {(32, 65536): 2421.7, (32, 131072): 2594.3, (8, 65536): 742.2,
+                               (8, 131072): 800.1}.items()],
+]
+
+
+def bench_sweep(steps: int, decode_steps: int) -> dict:
+    """Every SWEEP_PREFILL shape (non-causal and causal) and SWEEP_DECODE shape: checked against
+    fp64 first (prefill: 256 sampled rows of every (batch, head); decode: every sequence in full),
+    then timed (median of the event-timed steps; decode after a 1 GiB flush per step), with the
+    roofline fraction and the reference's H100 figure beside each."""
+    import torch
+
+    import flash_lab
+    from oracle import c_oracle, reference
+
+    prefill = []
+    for (b, h, hkv, sq, d), ref_tflops, source in SWEEP_PREFILL:
+        cfg = dict(batch=b, heads=h, heads_kv=hkv, seqlen=sq, head_dim=d)
+        for causal, ref in zip((False, True), ref_tflops):
+            print(f"# sweep prefill {cfg} causal={causal}", file=sys.stderr, flush=True)
+            r = bench_prefill(steps, 3, causal, False, cfg, label="sweep_prefill", clocks=False)
+            row = {"config": {**cfg, "causal": causal}, "status": r["status"],
+                   "reference_h100": {"tflops": ref, "source": source}}
+            if r["status"] == "ok":
+                row.update(tflops=r["tflops"], frac_of_peak=r["frac_of_peak"], ms=r["ms"]["median"],
+                           vs_reference=r["tflops"] / ref, max_err_vs_fp64=r["max_err_vs_fp64"],
+                           max_err_torch_vs_fp64=r["max_err_torch_vs_fp64"])
+            prefill.append(row)
+    decode = []
+    flush = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda")
+    for (b, h, hkv, ctx, d), ref_gbps, source in SWEEP_DECODE:
+        print(f"# sweep decode B={b} H={h} H_kv={hkv} ctx={ctx} D={d}", file=sys.stderr, flush=True)
+        gen = torch.Generator(device="cuda").manual_seed(0)
+        q = torch.randn(b, 1, h, d, generator=gen, device="cuda", dtype=torch.bfloat16)
+        k_cache = torch.randn((b, ctx, hkv, d), generator=gen, device="cuda", dtype=torch.bfloat16)
+        v_cache = torch.randn((b, ctx, hkv, d), generator=gen, device="cuda", dtype=torch.bfloat16)
+        lens = torch.full((b,), ctx, dtype=torch.int32, device="cuda")
+        out = flash_lab.decode(q, k_cache, v_cache, lens)
+        qc, kc, vc, lc = q.cpu(), k_cache.cpu(), v_cache.cpu(), lens.cpu()
+        ref, _ = c_oracle.decode(qc, kc, vc, lc)
+        plain = reference.decode(qc, kc, vc, lc, dtype=torch.bfloat16)
+        err = (out.cpu().double() - ref).abs().max().item()
+        err_torch = (plain.double() - ref).abs().max().item()
+        row = {"config": dict(batch=b, heads=h, heads_kv=hkv, context=ctx, head_dim=d),
+               "reference_h100": {"gbps_with_q_o": ref_gbps, "source": source},
+               "max_err_vs_fp64": err, "max_err_torch_vs_fp64": err_torch}
+        if not (bool(torch.isfinite(out).all()) and err <= 2 * err_torch + FLOOR_BF16):
+            decode.append({**row, "status": "incorrect"})
+            continue
+        times, _ = time_op(lambda: flash_lab.decode(q, k_cache, v_cache, lens), decode_steps, 10,
+                           flush, label="sweep_decode")
+        ms = summarize(times)["median"]
+        kv = decode_kv_bytes(b, hkv, ctx, d, 2)
+        with_qo = decode_bytes_with_qo(b, h, hkv, ctx, d, 2)
+        row.update(status="ok", ms=ms, gbps=kv / ms / 1e6, gbps_with_q_o=with_qo / ms / 1e6,
+                   frac_of_peak=kv / ms / 1e6 / PEAK_HBM_GBPS,
+                   vs_reference=with_qo / ms / 1e6 / ref_gbps)
+        decode.append(row)
+        del q, k_cache, v_cache, out
+        torch.cuda.empty_cache()
+    del flush
+    torch.cuda.empty_cache()
+    bad = [r for r in prefill + decode if r["status"] != "ok"]
+    return {"status": "incorrect" if bad else "ok", "prefill": prefill, "decode": decode}
 
 
 # Config L, the reference's end-to-end figures (bench/results/h100-80gb-hbm3/summary-cc64b18.md:
@@ -445,6 +661,24 @@ E2E_REFERENCE = {"ttft_ms_triton_prefill": 274.8, "ttft_ms_mma_pipelined": 311.7
                  "decode_step_ms": 9.58, "hardware": "H100 SXM5, real Llama-3.1-8B weights"}
 E2E_PROMPT = 8192
 E2E_NEW_TOKENS = 256
+
+
+def tokens_follow_sdpa(tokens, ref_tokens, ref_logits) -> dict:
+    """The reference's rule for greedy tokens (tests/test_e2e_llama.py:94-106): equal to SDPA's
+    up to the first step where they differ, which must be a near-tie of SDPA's top two logits
+    (within two bf16 steps of the larger); nothing after that step is compared."""
+    import torch
+
+    n = min(len(tokens), len(ref_tokens))
+    differ = (tokens[:n].cpu() != ref_tokens[:n].cpu()).nonzero()
+    out = {"tokens_checked": n, "first_difference": None, "tokens_follow_sdpa": True}
+    if len(differ):
+        step = int(differ[0])
+        first, second = ref_logits[step].float().topk(2).values.tolist()
+        tie = 2 * torch.finfo(torch.bfloat16).eps * 2 ** math.floor(math.log2(abs(first)))
+        out.update(first_difference=step, margin=first - second, near_tie=tie,
+                   tokens_follow_sdpa=first - second <= tie)
+    return out
 
 
 def bench_e2e_l(budget_s: float) -> dict:
@@ -481,9 +715,28 @@ def bench_e2e_l(budget_s: float) -> dict:
     check = {"max_logit_err_vs_fp32": err, "max_logit_err_sdpa_vs_fp32": err_torch}
     if not err <= 2 * err_torch + FLOOR_BF16:
         return {"status": "incorrect", "config": config, **check}
+    # The reference's token rule (tests/test_e2e_llama.py:94-135): the 256 greedy tokens of the
+    # compiled static-cache run follow SDPA's, up to a step where SDPA's own top two logits are
+    # within two bf16 steps of each other.
+    print("# e2e_L: sdpa greedy tokens", file=sys.stderr, flush=True)
+    model.set_attn_implementation("sdpa")
+    with torch.no_grad():
+        sdpa_out = model.generate(
+            ids, attention_mask=torch.ones_like(ids), max_new_tokens=E2E_NEW_TOKENS,
+            min_new_tokens=E2E_NEW_TOKENS, do_sample=False, temperature=None, top_p=None,
+            pad_token_id=eos, return_dict_in_generate=True, output_logits=True,
+        )
+    sdpa_tokens = sdpa_out.sequences[0, ids.shape[1]:]
+    sdpa_logits = torch.stack(sdpa_out.logits)[:, 0]
+    del sdpa_out
+    model.set_attn_implementation(name)
     torch._dynamo.reset()
     print("# e2e_L: warmup generation (compiles the decode step)", file=sys.stderr, flush=True)
-    e2e.generate(model, ids, E2E_NEW_TOKENS, eos, progress_every=64)
+    tokens, _ = e2e.generate(model, ids, E2E_NEW_TOKENS, eos, progress_every=64)
+    check.update(tokens_follow_sdpa(tokens[0], sdpa_tokens, sdpa_logits))
+    del sdpa_logits
+    if not check["tokens_follow_sdpa"]:
+        return {"status": "incorrect", "config": config, **check}
     warm_s = time.perf_counter() - t_start
     runs = []
     for i in range(2):
@@ -531,16 +784,19 @@ def parse_args(argv=None):
                              "then include a synchronize per step)")
     parser.add_argument(
         "--only",
-        help="comma list of workloads to run: prefill, prefill_causal, decode (all of them), "
-        f"{', '.join(DECODE)}, e2e_L, copy (a 1 GiB device copy, the calibration of the traffic "
-        "counters), gemm (a dense bf16 hipBLASLt GEMM), mfma (register-only MFMA chains: the "
-        "matrix pipes' rate under the power limit); default: all but copy, gemm and mfma",
+        help="comma list of workloads to run: prefill, prefill_causal, prefill_d64, "
+        f"prefill_d64_causal, decode (all of them), {', '.join(DECODE)}, e2e_L, sweep (the "
+        "reference's other benchmark shapes, prefill and decode, beside its H100 figures), copy (a "
+        "1 GiB device copy, the calibration of the traffic counters), gemm (a dense bf16 hipBLASLt "
+        "GEMM), mfma (register-only MFMA chains: the matrix pipes' rate under the power limit); "
+        "default: all but sweep, copy, gemm and mfma",
     )
     return parser.parse_args(argv)
 
 
 def selected_workloads(only: str | None, e2e: bool = True) -> list[str]:
-    everything = ["prefill", "prefill_causal", *DECODE] + (["e2e_L"] if e2e else [])
+    everything = (["prefill", "prefill_causal", "prefill_d64", "prefill_d64_causal", *DECODE]
+                  + (["e2e_L"] if e2e else []))
     if not only:
         return everything
     names = []
@@ -548,7 +804,7 @@ def selected_workloads(only: str | None, e2e: bool = True) -> list[str]:
         item = item.strip()
         if item == "decode":
             names += list(DECODE)
-        elif item in everything or item in ("copy", "gemm", "mfma", "e2e_L"):
+        elif item in everything or item in ("copy", "gemm", "mfma", "e2e_L", "sweep"):
             names.append(item)
         else:
             raise SystemExit(f"unknown workload {item!r}")
@@ -594,32 +850,37 @@ def bench_gemm(steps: int) -> dict:
 
 
 def bench_mfma_rate(steps: int) -> dict:
-    """The library's matrix-pipe rate probe (fl_mfma_rate_probe): one workgroup of 8 waves per CU
+    """The matrix-pipe rate probe (flc_mfma_rate_probe of the calibration library calib/, built
+    here if it is missing; not part of the product library): one workgroup of 8 waves per CU
     running v_mfma_f32_32x32x16_bf16 chains with nothing else beside them, on pseudo-random
     operands shaped like N(0,1) draws, on zeros, and on random operands whose A side is read from
     LDS for every MFMA (the prefill kernel's fragment traffic, 1 KiB per wave per MFMA). The MFMA
     rate the board's power limit leaves on random data, before and with the LDS traffic: the
     ceiling the prefill kernel is held under."""
     import torch
-    from flash_lab import _hip
 
+    import calib
+
+    lib = calib.load()
     workgroups, iters = 256, 6000
     out = torch.empty(workgroups * 512, device="cuda")
     flops = float(workgroups) * 8 * iters * 16 * 32768
 
     def run(flags):
         stream = torch.cuda.current_stream().cuda_stream
-        if _hip.LIB.fl_mfma_rate_probe(out.data_ptr(), workgroups, iters, flags, stream) != 0:
-            raise RuntimeError(_hip.LIB.fl_last_error().decode())
+        if lib.flc_mfma_rate_probe(out.data_ptr(), workgroups, iters, flags, stream) != 0:
+            raise RuntimeError(lib.flc_last_error().decode())
 
     result = {"status": "ok", "workgroups": workgroups, "waves_per_workgroup": 8, "iters": iters,
-              "flops": flops, "instruction": "v_mfma_f32_32x32x16_bf16"}
-    for label, flags in (("random", 0), ("zeros", _hip.PROBE_ZERO_OPERANDS),
-                         ("random_lds_a", _hip.PROBE_LDS_A)):
+              "flops": flops, "instruction": "v_mfma_f32_32x32x16_bf16",
+              "library": str(calib.OUTPUT.relative_to(REPO))}
+    for label, flags in (("random", 0), ("zeros", calib.PROBE_ZERO_OPERANDS),
+                         ("random_lds_a", calib.PROBE_LDS_A)):
         times, _ = time_op(lambda: run(flags), steps, 5, label=f"mfma_{label}")
         ms = summarize(times)
         result[label] = {"ms": ms, "tflops": flops / ms["median"] / 1e9,
-                         "frac_of_peak": flops / ms["median"] / 1e9 / PEAK_BF16_TFLOPS}
+                         "frac_of_peak": flops / ms["median"] / 1e9 / PEAK_BF16_TFLOPS,
+                         "gpu_clocks": gpu_window(lambda: run(flags), ms["median"])}
     return result
 
 
@@ -658,6 +919,7 @@ def main(argv=None) -> int:
     cpu = not args.no_cpu_baseline
     cpu_record = cpu_setup() if cpu else None
     props = torch.cuda.get_device_properties(0)
+    env = guarded("env", env_record)
     workloads = selected_workloads(args.only, e2e=not args.no_e2e)
     secondary = {}
     headline = None
@@ -677,6 +939,11 @@ def main(argv=None) -> int:
             "prefill_causal", lambda: bench_prefill(args.steps, args.warmup, True, cpu))
         print(f"# prefill causal: {json.dumps(secondary['prefill_causal'])}", file=sys.stderr,
               flush=True)
+    for name, causal in (("prefill_d64", False), ("prefill_d64_causal", True)):
+        if name in workloads:
+            secondary[name] = guarded(name, lambda: bench_prefill(
+                args.steps, args.warmup, causal, False, PREFILL_D64, label=name))
+            print(f"# {name}: {json.dumps(secondary[name])}", file=sys.stderr, flush=True)
     decodes = [name for name in DECODE if name in workloads]
     if decodes:
         flush = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda")
@@ -687,6 +954,9 @@ def main(argv=None) -> int:
                   flush=True)
         del flush
         torch.cuda.empty_cache()
+    if "sweep" in workloads:
+        secondary["sweep"] = guarded("sweep", lambda: bench_sweep(10, 50))
+        print(f"# sweep: {json.dumps(secondary['sweep'])}", file=sys.stderr, flush=True)
     if "copy" in workloads:
         secondary["copy"] = bench_copy(args.steps)
         print(f"# copy: {json.dumps(secondary['copy'])}", file=sys.stderr, flush=True)
@@ -712,6 +982,7 @@ def main(argv=None) -> int:
             "traffic": profiled_traffic(),
             "traffic_source": str(TRAFFIC_PROFILE.relative_to(REPO)),
             "kernel": "prefill_pp_kernel<bf16_tag, 128>",
+            "gfx_mhz_median": (headline.get("gpu_clocks") or {}).get("gfx_mhz", {}).get("median"),
             "per_launch": f"{headline['flops']:.4g} FLOP (4 B H S^2 D), mean {headline['mean_ms']:.4f} ms",
         }
     else:
@@ -765,9 +1036,13 @@ def main(argv=None) -> int:
         },
         "roofline": roofline,
         "cpu_baseline": cpu_baseline,
+        # The headline leg's own record: its check, step-time distribution and the GPU clock and
+        # power sampled over a second of the same work.
+        "headline": headline,
         "secondary": secondary,
         "device": {"name": props.name, "cus": props.multi_processor_count,
                    "arch": getattr(props, "gcnArchName", "")},
+        "env": env,
     }
     print(json.dumps(result), flush=True)
     return overall_status(headline, secondary)

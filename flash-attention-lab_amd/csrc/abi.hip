@@ -1,5 +1,6 @@
 // The C ABI declared in include/flash_lab_hip.h: argument checks, parameter derivation and
-// kernel launch. Host code only (the kernels live in prefill_fwd.hip, decode.hip, smoke.hip).
+// kernel launch. Host code only (the kernels live in prefill_fwd.hip, prefill_pp.hip, decode.hip,
+// decode_mfma.hip and smoke.hip).
 //
 // The checks restate the reference's op-boundary checks (csrc/common/attn_host.h:18-50,
 // csrc/decode/decode_host.h:18-53, csrc/decode/decode.cu:286-293) on plain pointers and strides;
@@ -17,9 +18,9 @@
 namespace {
 
 // Routing overrides (fl_set_knob); -1 = the built-in rule.
-std::atomic<int> g_knobs[FL_KNOB_COUNT] = {-1, -1, -1};
-constexpr int64_t kKnobMin[FL_KNOB_COUNT] = {0, 1, 1};
-constexpr int64_t kKnobMax[FL_KNOB_COUNT] = {int64_t{1} << 30, int64_t{1} << 20, 64};
+std::atomic<int> g_knobs[FL_KNOB_COUNT] = {-1, -1, -1, -1};
+constexpr int64_t kKnobMin[FL_KNOB_COUNT] = {0, 1, 1, 1};
+constexpr int64_t kKnobMax[FL_KNOB_COUNT] = {int64_t{1} << 30, int64_t{1} << 20, 64, 4};
 
 thread_local std::string g_last_error;
 
@@ -140,6 +141,8 @@ constexpr int kMfmaSpan = 4;
 constexpr int kMfmaSpanSplitKeys = 1024;
 int mfma_span(const fl_decode_params* p, const fl::DecodeLayout& layout, int num_splits) {
   if (!layout.mfma || p->heads_kv % kMfmaSpan != 0) return 1;
+  const int forced = fl::knob(FL_KNOB_DECODE_MFMA_SPAN);
+  if (forced >= 1) return forced == kMfmaSpan ? kMfmaSpan : 1;
   const int64_t wg = static_cast<int64_t>(p->batch) * (p->heads_kv / kMfmaSpan) * num_splits;
   const bool long_splits = num_splits == 1 || p->max_seqlen / num_splits >= kMfmaSpanSplitKeys;
   return wg >= kMinSpanWorkgroups && long_splits ? kMfmaSpan : 1;
@@ -492,21 +495,6 @@ int fl_mfma_tile_test(const void* a, const void* b, float* c, int32_t k, int32_t
       fl::launch_mfma_tile_test(static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), c,
                                 k, trans_b != 0, static_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail(FL_ERR_LAUNCH, std::string("tile test launch: ") + hipGetErrorString(err));
-  return FL_OK;
-}
-
-int fl_mfma_rate_probe(float* out, int32_t workgroups, int32_t iters, int32_t flags,
-                       fl_stream_t stream) {
-  if (workgroups < 1 || workgroups > 65536) return fail(FL_ERR_INVALID, "workgroups must be in [1, 65536]");
-  if (iters < 1 || iters > (1 << 20)) return fail(FL_ERR_INVALID, "iters must be in [1, 2^20]");
-  if (flags < 0 || flags > (FL_PROBE_ZERO_OPERANDS | FL_PROBE_LDS_A))
-    return fail(FL_ERR_INVALID, "unknown probe flags");
-  if (!out) return fail(FL_ERR_INVALID, "null output pointer");
-  const hipError_t err = fl::launch_mfma_rate(out, workgroups, iters,
-                                              (flags & FL_PROBE_ZERO_OPERANDS) != 0,
-                                              (flags & FL_PROBE_LDS_A) != 0,
-                                              static_cast<hipStream_t>(stream));
-  if (err != hipSuccess) return fail(FL_ERR_LAUNCH, std::string("rate probe launch: ") + hipGetErrorString(err));
   return FL_OK;
 }
 

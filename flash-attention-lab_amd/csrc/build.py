@@ -11,6 +11,9 @@ from __future__ import annotations
 
 import argparse
 import concurrent.futures
+import datetime
+import hashlib
+import json
 import os
 import shutil
 import subprocess
@@ -91,7 +94,41 @@ def build(
     _run([compiler, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)],
          verbose)
     os.replace(tmp, output)
+    write_build_record(output, compiler, defines)
     return output
+
+
+def _git(*args: str) -> str | None:
+    try:
+        proc = subprocess.run(["git", "-C", str(REPO), *args], capture_output=True, text=True,
+                              timeout=10)
+    except (OSError, subprocess.TimeoutExpired):
+        return None
+    return proc.stdout.strip() if proc.returncode == 0 else None
+
+
+def write_build_record(output: Path, compiler: str, defines: tuple[str, ...]) -> Path:
+    """<library>.build.json beside the library: the source it was built from (git HEAD and whether
+    the tree differed from it, plus a hash of the kernel sources and the header), the compiler
+    and the flags. It travels with the library, so a benchmark run on another machine, where
+    the checkout has no git metadata, can still say what it ran."""
+    digest = hashlib.sha256()
+    for path in sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.hpp"), *INCLUDE.glob("*.h")]):
+        digest.update(path.name.encode())
+        digest.update(path.read_bytes())
+    status = _git("status", "--porcelain", "--", str(CSRC), str(INCLUDE))
+    version = subprocess.run([compiler, "--version"], capture_output=True, text=True).stdout
+    record = {
+        "git_head": _git("rev-parse", "HEAD"),
+        "sources_differ_from_head": bool(status) if status is not None else None,
+        "sources_sha256": digest.hexdigest(),
+        "compiler": version.splitlines()[0] if version else compiler,
+        "flags": [*FLAGS, *(f"-D{d}" for d in defines)],
+        "built_at": datetime.datetime.now(datetime.timezone.utc).isoformat(timespec="seconds"),
+    }
+    path = output.with_suffix(".build.json")
+    path.write_text(json.dumps(record, indent=1) + "\n")
+    return path
 
 
 def main(argv=None) -> int:

@@ -113,9 +113,4 @@ hipError_t launch_axpy(const float* x, const float* y, float alpha, float* out, 
                        hipStream_t stream);
 hipError_t launch_mfma_tile_test(const uint16_t* a, const uint16_t* b, float* c, int k,
                                  int trans_b, hipStream_t stream);
-// workgroups x 512 threads of MFMA chains (A operands from registers or LDS); out holds one float
-// per thread.
-hipError_t launch_mfma_rate(float* out, int workgroups, int iters, bool zero, bool lds_a,
-                            hipStream_t stream);
-
 }  // namespace fl

@@ -99,10 +99,6 @@ class DecodeParams(ctypes.Structure):
     ]
 
 
-# fl_mfma_rate_probe flags (include/flash_lab_hip.h).
-PROBE_ZERO_OPERANDS = 1
-PROBE_LDS_A = 2
-
 # Every symbol include/flash_lab_hip.h declares, with its ctypes signature.
 SIGNATURES = {
     "fl_attention_fwd": (ctypes.c_int, [ctypes.POINTER(AttnParams), ctypes.c_void_p]),
@@ -141,10 +137,6 @@ SIGNATURES = {
             ctypes.c_void_p,
         ],
     ),
-    "fl_mfma_rate_probe": (
-        ctypes.c_int,
-        [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p],
-    ),
     "fl_set_knob": (ctypes.c_int, [ctypes.c_int32, ctypes.c_int64]),
     "fl_get_knob": (ctypes.c_int64, [ctypes.c_int32]),
     "fl_last_error": (ctypes.c_char_p, []),
@@ -180,7 +172,8 @@ def _check(rc: int) -> None:
 
 # Routing overrides of the library (enum fl_knob): test and experiment hooks that pin a call to
 # one of the kernels. None restores the built-in rule.
-KNOBS = {"prefill_pp_min_wg": 0, "decode_mfma_min_group": 1, "decode_wg_per_cu": 2}
+KNOBS = {"prefill_pp_min_wg": 0, "decode_mfma_min_group": 1, "decode_wg_per_cu": 2,
+         "decode_mfma_span": 3}
 
 
 def set_knob(name: str, value: int | None) -> None:

@@ -151,6 +151,33 @@ class ClockSampler:
         return out
 
 
+def driver_record(device_index: int = 0) -> dict | None:
+    """The GPU's driver and firmware identity and its power cap, read once through amdsmi (the
+    counterpart of the driver fields of the reference's bench/env.py:39-106); None without amdsmi
+    or a visible GPU."""
+    try:
+        import amdsmi
+    except ImportError:
+        return None
+    try:
+        amdsmi.amdsmi_init()
+        handle = amdsmi.amdsmi_get_processor_handles()[device_index]
+    except Exception:
+        return None
+    out: dict = {}
+    for key, call in (("driver", "amdsmi_get_gpu_driver_info"), ("vbios", "amdsmi_get_gpu_vbios_info"),
+                      ("power_cap", "amdsmi_get_power_cap_info"), ("asic", "amdsmi_get_gpu_asic_info")):
+        try:
+            info = getattr(amdsmi, call)(handle)
+        except Exception:
+            continue
+        if isinstance(info, dict):
+            out[key] = {k: v for k, v in info.items() if isinstance(v, (str, int, float))}
+    with contextlib.suppress(Exception):
+        amdsmi.amdsmi_shut_down()
+    return out
+
+
 _ROCTX = None
 _ROCTX_TRIED = False
 

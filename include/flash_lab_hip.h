@@ -166,24 +166,6 @@ int fl_mfma_tile_test(const void* a, const void* b, float* c, int32_t k, int32_t
                       fl_stream_t stream);
 
 /*
- * Matrix-pipe rate probe. No counterpart in the reference: a calibration
- * kernel for the prefill roofline. `workgroups` workgroups of 8 waves (two per
- * SIMD, one workgroup per CU) each run `iters` iterations of 16
- * v_mfma_f32_32x32x16_bf16 per wave. B operands come from registers; A
- * operands from registers, or with FL_PROBE_LDS_A from an LDS read per MFMA
- * (1 KiB per wave per MFMA, the prefill kernel's fragment traffic). Operands
- * are pseudo-random bf16 shaped like N(0,1) draws, or zeros with
- * FL_PROBE_ZERO_OPERANDS. Nothing else runs beside the MFMAs; one float per
- * thread is written to `out` (workgroups * 512 floats). FLOP per call:
- * workgroups * 8 * iters * 16 * 32768. workgroups in [1, 65536], iters in
- * [1, 2^20].
- */
-#define FL_PROBE_ZERO_OPERANDS 1
-#define FL_PROBE_LDS_A 2
-int fl_mfma_rate_probe(float* out, int32_t workgroups, int32_t iters, int32_t flags,
-                       fl_stream_t stream);
-
-/*
  * Routing overrides. No counterpart in the reference (its kernel choice is
  * fixed at build time): a test and experiment hook that pins a call to one
  * of this library's kernels, so the parity tests can run every shape on
@@ -199,12 +181,18 @@ int fl_mfma_rate_probe(float* out, int32_t workgroups, int32_t iters, int32_t fl
  *                                  never).
  *   FL_KNOB_DECODE_WG_PER_CU       [1, 64]: resident split workgroups per CU
  *                                  that fl_decode_plan assumes.
+ *   FL_KNOB_DECODE_MFMA_SPAN       [1, 4]: KV heads per workgroup of the
+ *                                  matrix-core decode kernel, 1 or 4 (4 only
+ *                                  where H_kv is a multiple of 4; other
+ *                                  values act as 1), whatever the size of
+ *                                  the call.
  */
 enum fl_knob {
   FL_KNOB_PREFILL_PP_MIN_WG = 0,
   FL_KNOB_DECODE_MFMA_MIN_GROUP = 1,
   FL_KNOB_DECODE_WG_PER_CU = 2,
-  FL_KNOB_COUNT = 3
+  FL_KNOB_DECODE_MFMA_SPAN = 3,
+  FL_KNOB_COUNT = 4
 };
 int fl_set_knob(int32_t knob, int64_t value);
 /* Current value of a knob (-1: the built-in rule), or -2 for an unknown knob. */

@@ -17,7 +17,7 @@ OUTPUT = HERE / "libattn_oracle.so"
 
 def build() -> Path:
     tmp = OUTPUT.with_suffix(".so.tmp")
-    cmd = ["gcc", "-O2", "-std=c11", "-fPIC", "-shared", str(SOURCE), "-o", str(tmp), "-lm"]
+    cmd = ["gcc", "-O3", "-std=c11", "-fopenmp", "-fPIC", "-shared", str(SOURCE), "-o", str(tmp), "-lm"]
     subprocess.run(cmd, check=True, capture_output=True, text=True)
     os.replace(tmp, OUTPUT)
     return OUTPUT

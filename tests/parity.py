@@ -17,7 +17,7 @@ import torch
 import torch.nn.functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
-from oracle import reference
+from oracle import c_oracle, reference
 
 FLOOR = {torch.float32: 1e-6, torch.bfloat16: 1e-3, torch.float16: 1e-3}
 GUARD = {torch.float32: 2e-5, torch.bfloat16: 2e-2, torch.float16: 1e-2}
@@ -54,13 +54,17 @@ class PrefillOracle:
     errors at the input dtype, and max |v|. Computed once, it can check several kernels' outputs
     for the same input. With `rows`, only those query rows (long sequences)."""
 
-    def __init__(self, q, k, v, causal, scale=None, rows=None):
+    def __init__(self, q, k, v, causal, scale=None, rows=None, c_ref=False):
         self.dtype = q.dtype
         self.shape = q.shape
         self.rows = rows
         qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
         if rows is None:
             self.ref, self.ref_lse = reference.attention(qc, kc, vc, causal, scale, return_lse=True)
+        elif c_ref:
+            # The oracle's C loops (oracle_attention_rows_f64, pinned to attention_rows at 1e-12):
+            # the same float64 rows without float64 copies of the long inputs.
+            self.ref, self.ref_lse = c_oracle.attention_rows(qc, kc, vc, rows, causal, scale)
         else:
             self.ref, self.ref_lse = reference.attention_rows(
                 qc, kc, vc, rows, causal, scale, return_lse=True
@@ -111,16 +115,22 @@ class PrefillOracle:
         return err, err_torch
 
 
-def check_prefill(out, lse, q, k, v, causal, scale=None, rows=None):
-    """Asserts the prefill rule; with `rows`, on those query rows only (long sequences)."""
-    return PrefillOracle(q, k, v, causal, scale, rows).check(out, lse)
+def check_prefill(out, lse, q, k, v, causal, scale=None, rows=None, c_ref=False):
+    """Asserts the prefill rule; with `rows`, on those query rows only (long sequences), the
+    float64 side from the oracle's C loops when c_ref is set."""
+    return PrefillOracle(q, k, v, causal, scale, rows, c_ref).check(out, lse)
 
 
-def check_decode(out, lse, q, k_cache, v_cache, seq_lens, scale=None):
-    """Asserts the decode rule against the oracle's per-sequence decode on the CPU."""
+def check_decode(out, lse, q, k_cache, v_cache, seq_lens, scale=None, c_ref=False):
+    """Asserts the decode rule against the oracle's per-sequence decode on the CPU. With c_ref the
+    float64 side comes from the oracle's C loops (oracle_decode_f64, pinned to the torch oracle
+    at 1e-12), which read a long bf16 cache without float64 copies."""
     dtype = q.dtype
     args = (q.cpu(), k_cache.cpu(), v_cache.cpu(), seq_lens.cpu())
-    ref, ref_lse = reference.decode(*args, softmax_scale=scale, return_lse=True)
+    if c_ref:
+        ref, ref_lse = c_oracle.decode(*args, softmax_scale=scale)
+    else:
+        ref, ref_lse = reference.decode(*args, softmax_scale=scale, return_lse=True)
     plain, plain_lse = reference.decode(*args, softmax_scale=scale, return_lse=True, dtype=dtype)
     out_c, lse_c = out.cpu(), lse.cpu()
     assert out.shape == q.shape and out.dtype == dtype and torch.isfinite(out_c).all()

@@ -59,7 +59,8 @@ def test_knobs_are_validated_and_restored(knobs):
     assert _hip.get_knob("decode_wg_per_cu") == 64
     for name, bad in (("decode_wg_per_cu", 0), ("decode_wg_per_cu", 65),
                       ("decode_mfma_min_group", 0), ("prefill_pp_min_wg", -5),
-                      ("prefill_pp_min_wg", (1 << 30) + 1)):
+                      ("prefill_pp_min_wg", (1 << 30) + 1), ("decode_mfma_span", 0),
+                      ("decode_mfma_span", 5)):
         with pytest.raises(RuntimeError, match="out of range"):
             _hip.set_knob(name, bad)
     assert _hip.LIB.fl_set_knob(7, 1) == 1 and b"unknown knob" in _hip.LIB.fl_last_error()
@@ -116,6 +117,21 @@ def test_decode_plan_routes_by_group(knobs):
     assert plan(8) == 16
     # One KV head per workgroup where four cannot fill the CUs with splits of >= 1024 keys.
     assert _hip.decode_plan(2, 32, 8, 128, 32768, torch.bfloat16)[0] == 16
+
+
+def test_decode_mfma_span_knob(knobs):
+    # The decode_mfma_span knob pins the matrix-core kernel's layout whatever the call's size:
+    # at 4 the plan takes the four-KV-heads split count (one workgroup per CU, splits of >= 1024
+    # keys where the cache allows), at 1 the one-KV-head plan.
+    plan = lambda b, s: _hip.decode_plan(b, 32, 8, 128, s, torch.bfloat16)[0]
+    assert plan(2, 32768) == 16 and plan(8, 32768) == 16
+    knobs("decode_mfma_span", 4)
+    assert plan(2, 32768) == 32  # 2 x 2 groups of four KV heads x 32 splits of 1024 keys
+    assert plan(1, 2048) == 2
+    knobs("decode_mfma_span", 1)
+    assert plan(8, 32768) == 4  # one KV head per workgroup: 64 x 4 fills 256 CUs
+    knobs("decode_mfma_span", None)
+    assert plan(8, 32768) == 16
 
 
 def test_decode_plan_requested_and_inplace():
@@ -251,15 +267,21 @@ def test_tile_test_rejects_bad_k():
     assert "K in {16, 32, 64}" in _hip.LIB.fl_last_error().decode()
 
 
-def test_rate_probe_rejects_bad_arguments():
-    assert _hip.LIB.fl_mfma_rate_probe(256, 0, 10, 0, None) != 0
-    assert "workgroups" in _hip.LIB.fl_last_error().decode()
-    assert _hip.LIB.fl_mfma_rate_probe(256, 8, 0, 0, None) != 0
-    assert "iters" in _hip.LIB.fl_last_error().decode()
-    assert _hip.LIB.fl_mfma_rate_probe(256, 8, 10, 4, None) != 0
-    assert "flags" in _hip.LIB.fl_last_error().decode()
-    assert _hip.LIB.fl_mfma_rate_probe(None, 8, 10, 0, None) != 0
-    assert "null" in _hip.LIB.fl_last_error().decode()
+def test_rate_probe_lives_outside_the_product_library():
+    # The calibration probe is built into calib/libfl_calib.so, which the product library does
+    # not contain; its argument checks run on the host.
+    import calib
+
+    assert not hasattr(_hip.LIB, "fl_mfma_rate_probe")
+    lib = calib.load()
+    assert lib.flc_mfma_rate_probe(256, 0, 10, 0, None) != 0
+    assert "workgroups" in lib.flc_last_error().decode()
+    assert lib.flc_mfma_rate_probe(256, 8, 0, 0, None) != 0
+    assert "iters" in lib.flc_last_error().decode()
+    assert lib.flc_mfma_rate_probe(256, 8, 10, 4, None) != 0
+    assert "flags" in lib.flc_last_error().decode()
+    assert lib.flc_mfma_rate_probe(None, 8, 10, 0, None) != 0
+    assert "null" in lib.flc_last_error().decode()
 
 
 def test_noalloc_decode_rejects_workspaces_beyond_its_scratch_array():

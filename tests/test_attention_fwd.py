@@ -118,7 +118,36 @@ def test_headline_shape_sampled_rows(causal):
     shape = (4, 4096, 32, 128)
     q, k, v = (torch.randn(shape, device="cuda", dtype=torch.bfloat16, generator=gen) for _ in range(3))
     out, lse = flash_lab.attention(q, k, v, causal=causal, return_lse=True)
-    check_prefill(out, lse, q, k, v, causal, rows=sampled_rows(4096, 256))
+    check_prefill(out, lse, q, k, v, causal, rows=sampled_rows(4096, 256), c_ref=True)
+
+
+# The other shapes of the reference's bf16 prefill benchmarks (bench/suites.py:63-94): prefill_bf16
+# (1K to 16K keys, head_dim 64, GQA with 8 KV heads) and prefill_seqlen (16K tokens per call,
+# S = 512 to 16384; its 4K, 8K and 16K rows are the ones above). (B, H, H_kv, S, D), bf16, seeded
+# like the benchmark, 256 sampled query rows of every (batch, head), causal and not.
+PREFILL_SUITE = [
+    (4, 32, 32, 1024, 128),
+    (2, 32, 32, 8192, 128),
+    (1, 32, 32, 16384, 128),
+    (8, 16, 16, 2048, 64),
+    (4, 32, 8, 4096, 128),
+    (32, 32, 32, 512, 128),
+    (16, 32, 32, 1024, 128),
+    (8, 32, 32, 2048, 128),
+]
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("shape", PREFILL_SUITE, ids=lambda s: f"B{s[0]}-H{s[1]}-Hkv{s[2]}-S{s[3]}-D{s[4]}")
+def test_reference_suite_shapes_sampled_rows(shape, causal):
+    batch, heads, heads_kv, seqlen, head_dim = shape
+    print(f"prefill suite shape {shape} causal={causal}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn(batch, seqlen, heads, head_dim, device="cuda", dtype=torch.bfloat16, generator=gen)
+    k = torch.randn(batch, seqlen, heads_kv, head_dim, device="cuda", dtype=torch.bfloat16, generator=gen)
+    v = torch.randn(batch, seqlen, heads_kv, head_dim, device="cuda", dtype=torch.bfloat16, generator=gen)
+    out, lse = flash_lab.attention(q, k, v, causal=causal, return_lse=True)
+    check_prefill(out, lse, q, k, v, causal, rows=sampled_rows(seqlen, 256), c_ref=True)
 
 
 def test_ragged_long_sequence_sampled_rows():

@@ -29,9 +29,13 @@ def test_summarize():
 
 
 def test_workload_selection():
-    assert bench.selected_workloads(None) == ["prefill", "prefill_causal", *bench.DECODE, "e2e_L"]
-    assert bench.selected_workloads(None, e2e=False) == ["prefill", "prefill_causal", *bench.DECODE]
+    prefills = ["prefill", "prefill_causal", "prefill_d64", "prefill_d64_causal"]
+    assert bench.selected_workloads(None) == [*prefills, *bench.DECODE, "e2e_L"]
+    assert bench.selected_workloads(None, e2e=False) == [*prefills, *bench.DECODE]
     assert bench.selected_workloads("decode,copy") == [*bench.DECODE, "copy"]
+    # The sweep of the reference's other suites runs only when asked for.
+    assert bench.selected_workloads("sweep") == ["sweep"]
+    assert "sweep" not in bench.selected_workloads(None)
     assert bench.selected_workloads("e2e_L", e2e=False) == ["e2e_L"]
     # The calibration legs (hipBLASLt GEMM, MFMA rate probe) run only when asked for.
     assert bench.selected_workloads("mfma,gemm,prefill") == ["mfma", "gemm", "prefill"]
@@ -87,6 +91,46 @@ def test_cpu_timer_respects_reps_and_budget():
     t = bench.time_cpu(lambda: None, budget_s=60.0, warmed_up=True)
     assert t["warmup"] == 0 and t["reps"] == bench.CPU_MAX_REPS
     assert set(t["ms"]) == {"median", "p10", "p90", "min"}
+
+
+def test_cpu_timer_minimum_reps():
+    t = bench.time_cpu(lambda: None, budget_s=0.0, warmed_up=True, min_reps=bench.CPU_DECODE_REPS)
+    assert t["reps"] == bench.CPU_DECODE_REPS >= 10
+
+
+def test_cpu_decode_leg_samples_two_sequences():
+    import torch
+
+    gen = torch.Generator().manual_seed(0)
+    q = torch.randn(4, 1, 8, 64, generator=gen).to(torch.bfloat16)
+    k = torch.randn(4, 300, 2, 64, generator=gen).to(torch.bfloat16)
+    lens = torch.tensor([300, 100, 200, 300], dtype=torch.int32)
+    leg = bench.cpu_decode_leg(q, k, k, lens)
+    assert leg["reps"] >= 10 and "2 of 4 sequences" in leg["sample"]
+    # GB/s of the bf16 K+V bytes of the two sequences it timed: 2 x (300 + 100) x 2 x 64 x 2 B.
+    assert leg["gbps"] == pytest.approx(2 * 400 * 2 * 64 * 2 / (leg["ms"]["median"] / 1e3) / 1e9)
+
+
+def test_sweep_tables_cover_the_reference_suites():
+    # bench/suites.py:63-125 of the reference: 9 prefill shapes (prefill_bf16 and prefill_seqlen),
+    # 16 decode_ctx + 3 decode_batch + 6 decode_d64 + 4 decode_long shapes.
+    assert len(bench.SWEEP_PREFILL) == 9 and len(bench.SWEEP_DECODE) == 29
+    assert len({shape for shape, _, _ in bench.SWEEP_DECODE}) == 29
+    assert all(v > 0 for _, pair, _ in bench.SWEEP_PREFILL for v in pair)
+
+
+def test_tokens_follow_sdpa_rule():
+    import torch
+
+    ref = torch.tensor([5, 6, 7, 8])
+    logits = torch.zeros(4, 10)
+    logits[2, 7], logits[2, 3] = 10.0, 10.0 - 1e-3  # a near-tie at step 2
+    same = bench.tokens_follow_sdpa(ref.clone(), ref, logits)
+    assert same["tokens_follow_sdpa"] and same["tokens_checked"] == 4 and same["first_difference"] is None
+    tie = bench.tokens_follow_sdpa(torch.tensor([5, 6, 3, 1]), ref, logits)
+    assert tie["tokens_follow_sdpa"] and tie["first_difference"] == 2
+    logits[1, 6], logits[1, 2] = 10.0, 9.0  # a clear winner at step 1
+    assert not bench.tokens_follow_sdpa(torch.tensor([5, 2, 7, 8]), ref, logits)["tokens_follow_sdpa"]
 
 
 def test_cpu_c1_leg_meets_the_fp32_rule():

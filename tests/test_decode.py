@@ -375,3 +375,108 @@ def test_paged_splits_longer_than_the_staged_table(impl):
     out, lse = flash_lab.decode(q, k_pool, v_pool, seq_lens, block_tables=tables, impl=impl,
                                 num_splits=splits, return_lse=True)
     check_decode(out, lse, q, k_cache, v_cache, seq_lens)
+
+
+# The decode shapes of the reference's other benchmark suites (bench/suites.py:76-125): contexts
+# of 512 to 8K keys for B in {1, 8} and H_kv in {32, 8} (decode_ctx; its 32K rows are above, plus
+# B=1 GQA at 32K, the reference's weakest row, bench/results/h100-80gb-hbm3/summary-cc64b18.md:82),
+# head_dim 64 with 8 KV heads (decode_d64), one sequence at 64K and 128K keys (decode_long) and
+# batches up to 64 at 2K keys (decode_batch). bf16 caches fully valid, seeded like the benchmark;
+# every sequence and head is checked in full against float64 (the oracle's C loops read the
+# bf16 cache in place).
+SUITE_SHAPES = sorted({
+    *[(b, 32, hkv, ctx, 128) for b in (1, 8) for hkv in (32, 8) for ctx in (512, 2048, 8192)],
+    (1, 32, 8, 32768, 128),
+    *[(b, 32, 8, ctx, 64) for b in (1, 8) for ctx in (2048, 8192, 32768)],
+    *[(1, 32, hkv, ctx, 128) for hkv in (32, 8) for ctx in (65536, 131072)],
+    *[(b, 32, 8, 2048, 128) for b in (4, 16, 64)],
+})
+
+
+@pytest.mark.parametrize("shape", SUITE_SHAPES, ids=lambda s: f"B{s[0]}-H{s[1]}-Hkv{s[2]}-S{s[3]}-D{s[4]}")
+def test_reference_suite_shapes(shape):
+    batch, heads, heads_kv, context, head_dim = shape
+    print(f"decode suite shape {shape}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn(batch, 1, heads, head_dim, device="cuda", dtype=torch.bfloat16, generator=gen)
+    cache_shape = (batch, context, heads_kv, head_dim)
+    k_cache = torch.randn(cache_shape, device="cuda", dtype=torch.bfloat16, generator=gen)
+    v_cache = torch.randn(cache_shape, device="cuda", dtype=torch.bfloat16, generator=gen)
+    seq_lens = torch.full((batch,), context, device="cuda", dtype=torch.int32)
+    # The planned split count, and at 64K keys and more also the largest (128 splits of 512 or
+    # 1024 keys), so the split arithmetic runs at the cap.
+    counts = [None, 128] if context >= 65536 else [None]
+    for num_splits in counts:
+        out, lse = flash_lab.decode(q, k_cache, v_cache, seq_lens, num_splits=num_splits,
+                                    return_lse=True)
+        check_decode(out, lse, q, k_cache, v_cache, seq_lens, c_ref=True)
+
+
+# The matrix-core kernel's four-KV-heads-per-workgroup layout (wave w takes KV head 4 q + w) is
+# chosen on the host only for calls large enough to fill the CUs with long splits; the
+# decode_mfma_span knob pins it on small shapes, so ragged and short lengths (a partial last tile,
+# sequences shorter than a split, empty splits), fp16, head_dim 64, one split and paged caches run
+# through it against the oracle.
+SPAN4_CASES = [
+    # batch, heads, heads_kv, max_seqlen, head_dim, seq_lens (heads_kv a multiple of 4)
+    (8, 32, 8, 3000, 128, [3000, 1, 500, 1777, 2048, 31, 999, 2999]),
+    (2, 64, 8, 2000, 64, [2000, 77]),  # head_dim 64, 8 query heads per KV head
+    (3, 16, 4, 1500, 128, [1500, 700, 3]),
+    (2, 128, 4, 600, 128, [600, 129]),  # 32 query heads per KV head
+]
+
+
+@pytest.fixture
+def span4(knobs):
+    knobs("decode_mfma_span", 4)
+
+
+@pytest.mark.parametrize("num_splits", [None, 1, 2, 8, 64])
+@pytest.mark.parametrize("dtype", DTYPES[:2], ids=lambda d: str(d).removeprefix("torch."))
+@pytest.mark.parametrize("case", SPAN4_CASES, ids=lambda c: f"B{c[0]}-H{c[1]}-Hkv{c[2]}-S{c[3]}-D{c[4]}")
+def test_four_kv_heads_per_workgroup(case, dtype, num_splits, span4):
+    print(f"decode (four KV heads per workgroup) {dtype} {case} splits={num_splits}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(20)
+    q, k_cache, v_cache, seq_lens = make_case(case, dtype, gen)
+    out, lse = flash_lab.decode(q, k_cache, v_cache, seq_lens, num_splits=num_splits,
+                                return_lse=True)
+    check_decode(out, lse, q, k_cache, v_cache, seq_lens)
+
+
+def test_four_kv_heads_per_workgroup_empty_sequence(span4):
+    # A sequence of length 0 gives zeros and -inf on every split; the others are unaffected.
+    gen = torch.Generator(device="cuda").manual_seed(21)
+    q, k_cache, v_cache, _ = make_case((3, 32, 8, 900, 128, [900, 900, 900]), torch.bfloat16, gen)
+    lens = torch.tensor([900, 0, 450], device="cuda", dtype=torch.int32)
+    for num_splits in (1, 4):
+        out, lse = flash_lab.decode(q, k_cache, v_cache, lens, num_splits=num_splits,
+                                    return_lse=True)
+        assert torch.all(out[1] == 0) and torch.isneginf(lse[1]).all()
+        keep = torch.tensor([0, 2], device="cuda")
+        check_decode(out[keep], lse[keep], q[keep], k_cache[keep], v_cache[keep], lens[keep])
+
+
+@pytest.mark.parametrize("num_splits", [1, 4, 32])
+def test_four_kv_heads_per_workgroup_paged_equals_contiguous_bitwise(num_splits, span4):
+    gen = torch.Generator(device="cuda").manual_seed(22)
+    q, k_cache, v_cache, seq_lens = make_case((3, 32, 8, 3000, 128, [3000, 17, 2048]),
+                                              torch.bfloat16, gen)
+    cpu_gen = torch.Generator().manual_seed(23)
+    k_pool, tables = to_paged(k_cache, 16, cpu_gen)
+    cpu_gen = torch.Generator().manual_seed(23)
+    v_pool, _ = to_paged(v_cache, 16, cpu_gen)
+    want = flash_lab.decode(q, k_cache, v_cache, seq_lens, num_splits=num_splits, return_lse=True)
+    got = flash_lab.decode(q, k_pool, v_pool, seq_lens, block_tables=tables,
+                           num_splits=num_splits, return_lse=True)
+    assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+    check_decode(want[0], want[1], q, k_cache, v_cache, seq_lens)
+
+
+def test_inplace_large_batch_takes_four_kv_heads_per_workgroup():
+    # decode_inplace (one split) with batch * H_kv = 2048: the default rule picks four KV heads
+    # per workgroup (512 workgroups) here, with no knob.
+    gen = torch.Generator(device="cuda").manual_seed(24)
+    q, k_cache, v_cache, seq_lens = make_case((256, 32, 8, 300, 128, "random"), torch.bfloat16, gen)
+    out, lse = flash_lab.decode(q, k_cache, v_cache, seq_lens, impl="decode_inplace",
+                                return_lse=True)
+    check_decode(out, lse, q, k_cache, v_cache, seq_lens)

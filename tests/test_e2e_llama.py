@@ -149,7 +149,7 @@ def test_static_cache_decode_compiles_in_one_graph(model, prompts, sdpa_runs):
 # prompt position at most twice as far from an fp32 copy of the weights as SDPA's, and greedy
 # tokens from the compiled static-cache decode step that follow SDPA's up to a near-tie.
 L_PROMPT = 8192
-L_NEW_TOKENS = 24
+L_NEW_TOKENS = 256  # the configured generation length
 
 
 @pytest.mark.timeout(900)

@@ -46,20 +46,21 @@ def test_key_order_over_64_keys(flash_ops):
 
 
 @pytest.mark.parametrize("lds_a", [False, True], ids=["registers", "lds"])
-def test_rate_probe_runs(flash_ops, lds_a):
-    # The calibration kernel behind bench.py's `mfma` leg: zero operands give exact zeros, random
-    # ones finite sums, the same on every call.
-    from flash_lab import _hip
+def test_rate_probe_runs(lds_a):
+    # The calibration kernel behind bench.py's `mfma` leg, from its own library (not the product
+    # one): zero operands give exact zeros, random ones finite sums, the same on every call.
+    import calib
 
-    flags = _hip.PROBE_LDS_A if lds_a else 0
+    lib = calib.load()
+    flags = calib.PROBE_LDS_A if lds_a else 0
     out = torch.full((8 * 512,), float("nan"), device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
-    assert _hip.LIB.fl_mfma_rate_probe(out.data_ptr(), 8, 3, flags | _hip.PROBE_ZERO_OPERANDS, stream) == 0
+    assert lib.flc_mfma_rate_probe(out.data_ptr(), 8, 3, flags | calib.PROBE_ZERO_OPERANDS, stream) == 0
     torch.cuda.synchronize()
     assert (out == 0).all()
-    assert _hip.LIB.fl_mfma_rate_probe(out.data_ptr(), 8, 3, flags, stream) == 0
+    assert lib.flc_mfma_rate_probe(out.data_ptr(), 8, 3, flags, stream) == 0
     first = out.clone()
-    assert _hip.LIB.fl_mfma_rate_probe(out.data_ptr(), 8, 3, flags, stream) == 0
+    assert lib.flc_mfma_rate_probe(out.data_ptr(), 8, 3, flags, stream) == 0
     torch.cuda.synchronize()
     assert torch.isfinite(first).all() and (first != 0).any()
     assert torch.equal(first, out)

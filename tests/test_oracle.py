@@ -295,6 +295,50 @@ def test_decode_matches_c_restatement():
         torch.testing.assert_close(lse[b], lse_c[0, :, 0], **EXACT)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_c_decode_reads_the_cache_dtype_and_matches_the_oracle(dtype):
+    # oracle_decode_f64 (the C loops the long-cache GPU checks use) reads bf16 / fp32 caches in
+    # place and must give the float64 decode of the same values: GQA, ragged lengths (1 and the
+    # full cache), rank-3 and rank-4 queries, an explicit scale.
+    gen = torch.Generator().manual_seed(7)
+    batch, max_seqlen, heads, heads_kv, head_dim = 3, 50, 8, 2, 32
+    k_cache = torch.randn(batch, max_seqlen, heads_kv, head_dim, generator=gen).to(dtype)
+    v_cache = torch.randn(batch, max_seqlen, heads_kv, head_dim, generator=gen).to(dtype)
+    q = torch.randn(batch, 1, heads, head_dim, generator=gen).to(dtype)
+    seq_lens = torch.tensor([50, 1, 17], dtype=torch.int32)
+    for query, scale in ((q, None), (q[:, 0], 0.37)):
+        want, want_lse = reference.decode(query, k_cache, v_cache, seq_lens, softmax_scale=scale,
+                                          return_lse=True)
+        got, got_lse = c_oracle.decode(query, k_cache, v_cache, seq_lens, softmax_scale=scale)
+        assert got.shape == want.shape and got.dtype == torch.float64
+        torch.testing.assert_close(got, want, **EXACT)
+        torch.testing.assert_close(got_lse, want_lse, **EXACT)
+    with pytest.raises(ValueError, match="rejected"):
+        c_oracle.decode(q, k_cache, v_cache, torch.tensor([50, 0, 3], dtype=torch.int32))
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("seqlen_q,seqlen_k", [(70, 50), (40, 90)], ids=["sq>sk", "sq<sk"])
+def test_c_rows_match_attention_rows(seqlen_q, seqlen_k, dtype, causal):
+    # oracle_attention_rows_f64 (the C loops the long prefill checks use) against attention_rows:
+    # GQA, both S_q != S_k directions (with causal rows that see no key), first and last rows.
+    gen = torch.Generator().manual_seed(8)
+    q = torch.randn(2, seqlen_q, 6, 32, generator=gen).to(dtype)
+    k = torch.randn(2, seqlen_k, 3, 32, generator=gen).to(dtype)
+    v = torch.randn(2, seqlen_k, 3, 32, generator=gen).to(dtype)
+    rows = torch.tensor([0, 5, 19, 20, 21, seqlen_q - 1])
+    want, want_lse = reference.attention_rows(q, k, v, rows, causal, 0.3, return_lse=True)
+    got, got_lse = c_oracle.attention_rows(q, k, v, rows, causal, 0.3)
+    assert got.shape == want.shape and got_lse.shape == want_lse.shape
+    torch.testing.assert_close(got, want, **EXACT)
+    assert torch.equal(torch.isneginf(got_lse), torch.isneginf(want_lse))
+    finite = torch.isfinite(want_lse)
+    torch.testing.assert_close(got_lse[finite], want_lse[finite], **EXACT)
+    with pytest.raises(ValueError, match="rejected"):
+        c_oracle.attention_rows(q, k, v, torch.tensor([0, seqlen_q]), causal)
+
+
 def test_paged_decode_matches_contiguous():
     batch, max_seqlen, heads, heads_kv, head_dim, page_size = 3, 16, 4, 1, 8, 4
     k_cache, v_cache = make_cache(batch, max_seqlen, heads_kv, head_dim)

@@ -69,3 +69,28 @@ def test_noalloc_paged_cache_and_one_split():
                                             num_splits=splits, return_lse=True)
         assert splits == num_splits
         assert torch.equal(o, want_o) and torch.equal(lse, want_lse)
+
+
+def test_noalloc_replays_in_a_graph():
+    # The entry point for code under graph capture: a first call outside the capture (it looks
+    # up the scratch array's address on this device), then a captured call, replayed after q and
+    # seq_lens change in place; each replay must give fl_decode's bits at the same split count.
+    q, k, v, seq_lens = make(2, 32, 8, 4096, 128, [4096, 1000], 30)
+    o = torch.empty_like(q)
+    lse = torch.empty(q.shape[:2], device="cuda", dtype=torch.float32)
+    splits = _hip.decode_noalloc(q, k, v, seq_lens, o, lse, 128 ** -0.5, 16)
+    assert splits == 16
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        _hip.decode_noalloc(q, k, v, seq_lens, o, lse, 128 ** -0.5, 16)
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    for lens in ([4096, 1000], [17, 4096], [2048, 1]):
+        q.copy_(torch.randn(q.shape, device="cuda", dtype=q.dtype, generator=gen))
+        seq_lens.copy_(torch.tensor(lens, device="cuda", dtype=torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        want_o, want_lse = flash_lab.decode(q, k, v, seq_lens, num_splits=16, return_lse=True)
+        torch.cuda.synchronize()
+        assert torch.equal(o, want_o) and torch.equal(lse, want_lse), lens
