@@ -919,7 +919,6 @@ def main(argv=None) -> int:
     cpu = not args.no_cpu_baseline
     cpu_record = cpu_setup() if cpu else None
     props = torch.cuda.get_device_properties(0)
-    env = guarded("env", env_record)
     workloads = selected_workloads(args.only, e2e=not args.no_e2e)
     secondary = {}
     headline = None
@@ -930,6 +929,8 @@ def main(argv=None) -> int:
         except Exception as exc:  # recorded and reported, never silently dropped
             print(f"# {label} failed: {exc!r}", file=sys.stderr, flush=True)
             return {"status": "error", "error": repr(exc)}
+
+    env = guarded("env", env_record)
 
     if "prefill" in workloads:
         headline = guarded("prefill", lambda: bench_prefill(args.steps, args.warmup, False, cpu))

@@ -18,9 +18,9 @@
 namespace {
 
 // Routing overrides (fl_set_knob); -1 = the built-in rule.
-std::atomic<int> g_knobs[FL_KNOB_COUNT] = {-1, -1, -1, -1};
-constexpr int64_t kKnobMin[FL_KNOB_COUNT] = {0, 1, 1, 1};
-constexpr int64_t kKnobMax[FL_KNOB_COUNT] = {int64_t{1} << 30, int64_t{1} << 20, 64, 4};
+std::atomic<int> g_knobs[FL_KNOB_COUNT] = {-1, -1, -1, -1, -1};
+constexpr int64_t kKnobMin[FL_KNOB_COUNT] = {0, 1, 1, 1, 0};
+constexpr int64_t kKnobMax[FL_KNOB_COUNT] = {int64_t{1} << 30, int64_t{1} << 20, 64, 4, 1};
 
 thread_local std::string g_last_error;
 

@@ -27,7 +27,8 @@ INCLUDE = REPO / "include"
 BUILD_DIR = CSRC / "_build"
 OUTPUT = PKG_ROOT / "flash_lab" / "libflash_lab_hip.so"
 
-SOURCES = ("abi.hip", "prefill_fwd.hip", "prefill_pp.hip", "decode.hip", "decode_mfma.hip", "smoke.hip")
+SOURCES = ("abi.hip", "prefill_fwd.hip", "prefill_pp.hip", "prefill_causal.hip", "decode.hip",
+           "decode_mfma.hip", "smoke.hip")
 ARCH = "gfx950"
 FLAGS = (
     f"--offload-arch={ARCH}",

@@ -87,9 +87,13 @@ constexpr int kPrefillBlockM = 128;
 constexpr int kPrefillBlockN = 64;
 
 hipError_t launch_prefill(const PrefillArgs& args, DType dtype, int head_dim, hipStream_t stream);
-// Ping-pong variant (head_dim 128 only): 8 waves, 256 query rows per workgroup.
+// Ping-pong variant (head_dim 128 and 64): 8 waves, 256 query rows per workgroup.
 hipError_t launch_prefill_pingpong(const PrefillArgs& args, DType dtype, int head_dim,
                                    hipStream_t stream);
+// The same kernel for causal calls with a pair of query blocks per workgroup run as one stream of
+// key tiles (prefill_causal.hip); launch_prefill_pingpong routes causal calls to it.
+hipError_t launch_prefill_causal_stream(const PrefillArgs& args, DType dtype, int head_dim,
+                                        hipStream_t stream);
 
 // How decode work is laid out. The vector kernel (decode.hip): each workgroup serves heads_per_wg
 // query heads (a power of two dividing the GQA group) of each of kv_span adjacent KV heads. The

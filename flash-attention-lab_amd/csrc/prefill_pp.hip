@@ -39,80 +39,12 @@
 //    XCDs, each with its own L2); causal query blocks in heavy/light pairs per workgroup.
 #include <type_traits>
 
-#include "launch.hpp"
-#include "prefill_tile.hpp"
+#include "prefill_pp.hpp"
 
 namespace fl {
 namespace prefill {
 namespace pp {
 namespace {
-
-constexpr int kPpWaves = 8;
-constexpr int kPpThreads = 64 * kPpWaves;
-constexpr int kPpBlockM = kRowsPerWave * kPpWaves;  // 256 query rows per workgroup
-constexpr int kLoadWaves = 4;                       // waves per group: one group per tensor
-constexpr int kXcds = 8;
-constexpr float kLn2 = 0.693147180559945309f;
-// Largest lane sum of probabilities (32 of them) kept without moving the reference point.
-constexpr float kSumLimit = 32768.f;
-// Reference point of a row that has not seen a score yet: finite, so p = 2^(s scale_log2 - ref)
-// overflows (sum above kSumLimit: the first tile with a key takes the max path) and masked scores
-// still give 0, with no separate test for "no reference yet".
-constexpr float kNoRef = -1e30f;
-
-// LDS ring depth (K and V slots each). A K tile is issued kStages - 1 periods before the period
-// that first reads it, a V tile kStages - 2 (in the second half of its period).
-#ifndef FL_PP_STAGES
-#define FL_PP_STAGES 4
-#endif
-constexpr int kStages = FL_PP_STAGES;
-static_assert(kStages == 3 || kStages == 4, "3 or 4 ring stages");
-// Raise the issue priority of the wave in its MFMA phase (1) or in its softmax phase (2).
-#ifndef FL_PP_SETPRIO
-#define FL_PP_SETPRIO 1
-#endif
-// MFMAs whose A-operand fragments are in flight ahead of the one issuing. Two keep the MFMA phase
-// as fast as four did and leave the registers that the peeled first and last periods need (with
-// four, the kernel spilled at head_dim 128).
-#ifndef FL_PP_AHEAD
-#define FL_PP_AHEAD 2
-#endif
-
-__device__ __forceinline__ float max_of(const f32x16& x, const f32x16& y) {
-  float t[11];
-#pragma unroll
-  for (int i = 0; i < 5; ++i) t[i] = fmaxf(fmaxf(x[3 * i], x[3 * i + 1]), x[3 * i + 2]);
-#pragma unroll
-  for (int i = 0; i < 5; ++i) t[5 + i] = fmaxf(fmaxf(y[3 * i], y[3 * i + 1]), y[3 * i + 2]);
-  t[10] = fmaxf(x[15], y[15]);
-  const float u0 = fmaxf(fmaxf(t[0], t[1]), t[2]);
-  const float u1 = fmaxf(fmaxf(t[3], t[4]), t[5]);
-  const float u2 = fmaxf(fmaxf(t[6], t[7]), t[8]);
-  const float u3 = fmaxf(t[9], t[10]);
-  return fmaxf(fmaxf(u0, u1), fmaxf(u2, u3));
-}
-
-__device__ __forceinline__ int xcd_remap(int id, int n) {
-  const int per = n / kXcds;
-  if (id >= per * kXcds) return id;
-  return (id % kXcds) * per + id / kXcds;
-}
-
-// Workgroup barrier without a memory fence: LDS reads are complete before it (lgkmcnt(0)); loads
-// into LDS are waited for explicitly by the waves that issued them. The sched_barriers keep the
-// compiler from moving any instruction across it.
-__device__ __forceinline__ void phase_barrier() {
-  __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-// Waits until at most kCount of this wave's vector-memory loads are in flight.
-template <int kCount>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(kCount >= 0 && kCount <= 63, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kCount) : "memory");
-}
 
 template <typename Tag, int D>
 __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -632,6 +564,8 @@ hipError_t launch_typed(PrefillArgs args, hipStream_t stream) {
 hipError_t launch_prefill_pingpong(const PrefillArgs& args, DType dtype, int head_dim,
                                    hipStream_t stream) {
   using namespace prefill::pp;
+  if (args.causal && knob(FL_KNOB_PREFILL_CAUSAL_STREAM) != 0)
+    return launch_prefill_causal_stream(args, dtype, head_dim, stream);
   if (head_dim == 64) {
     return dtype == DType::bf16 ? launch_typed<bf16_tag, 64>(args, stream)
                                 : launch_typed<f16_tag, 64>(args, stream);

@@ -173,7 +173,7 @@ def _check(rc: int) -> None:
 # Routing overrides of the library (enum fl_knob): test and experiment hooks that pin a call to
 # one of the kernels. None restores the built-in rule.
 KNOBS = {"prefill_pp_min_wg": 0, "decode_mfma_min_group": 1, "decode_wg_per_cu": 2,
-         "decode_mfma_span": 3}
+         "decode_mfma_span": 3, "prefill_causal_stream": 4}
 
 
 def set_knob(name: str, value: int | None) -> None:

@@ -186,13 +186,18 @@ int fl_mfma_tile_test(const void* a, const void* b, float* c, int32_t k, int32_t
  *                                  where H_kv is a multiple of 4; other
  *                                  values act as 1), whatever the size of
  *                                  the call.
+ *   FL_KNOB_PREFILL_CAUSAL_STREAM  [0, 1]: how the 8-wave kernel runs a
+ *                                  causal pair of query blocks: 1 = one
+ *                                  stream of key tiles (the default), 0 = two
+ *                                  blocks one after the other.
  */
 enum fl_knob {
   FL_KNOB_PREFILL_PP_MIN_WG = 0,
   FL_KNOB_DECODE_MFMA_MIN_GROUP = 1,
   FL_KNOB_DECODE_WG_PER_CU = 2,
   FL_KNOB_DECODE_MFMA_SPAN = 3,
-  FL_KNOB_COUNT = 4
+  FL_KNOB_PREFILL_CAUSAL_STREAM = 4,
+  FL_KNOB_COUNT = 5
 };
 int fl_set_knob(int32_t knob, int64_t value);
 /* Current value of a knob (-1: the built-in rule), or -2 for an unknown knob. */

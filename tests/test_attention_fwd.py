@@ -35,6 +35,11 @@ SHAPES = [
     (1, 101, 37, 4, 4, 128),  # S_q > S_k: causal rows without keys
     (1, 700, 300, 2, 1, 128),  # S_q > S_k over three blocks: a block, and waves, with no keys
     (2, 1, 300, 8, 2, 128),
+    # Causal pairs of 256-row blocks whose waves switch from the light to the heavy block with 1,
+    # 2 or 3 idle periods, or none, or have no heavy keys (the one-stream schedule's cases).
+    (2, 900, 1000, 8, 2, 128),
+    (1, 481, 482, 4, 4, 64),
+    (2, 355, 131, 4, 2, 128),
 ]
 SLOW_SHAPES = [(1, 4096, 4096, 4, 4, 128), (1, 8192, 8192, 2, 1, 64)]
 
@@ -58,13 +63,25 @@ def sampled_rows(seqlen, count, seed=0):
 
 # The library runs the 8-wave ping-pong kernel when it fills at least 256 workgroups and the
 # 4-wave kernel below that (head_dim 64 and 128 alike); the prefill_pp_min_wg knob routes a shape
-# to either one, so both are checked on every shape.
-ROUTES = {"auto": None, "pingpong": 0, "wg128": 1 << 30}
+# to either one, so both are checked on every shape. The ping-pong kernel runs a causal pair of
+# query blocks as one stream of key tiles (prefill_causal.hip, the default) or as two blocks
+# (prefill_pp.hip, the prefill_causal_stream knob at 0): "pp_blocks" checks the second.
+ROUTES = {
+    "auto": {},
+    "pingpong": {"prefill_pp_min_wg": 0},
+    "pp_blocks": {"prefill_pp_min_wg": 0, "prefill_causal_stream": 0},
+    "wg128": {"prefill_pp_min_wg": 1 << 30},
+}
+
+
+def set_route(knobs, name):
+    for knob, value in ROUTES[name].items():
+        knobs(knob, value)
 
 
 @pytest.fixture(params=list(ROUTES), ids=str)
 def route(request, knobs):
-    knobs("prefill_pp_min_wg", ROUTES[request.param])
+    set_route(knobs, request.param)
     return request.param
 
 
@@ -96,22 +113,29 @@ def _long_case(shape, dtype, causal):
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("kernel", ["pingpong", "wg128"])
+@pytest.mark.parametrize("kernel", ["pingpong", "pp_blocks", "wg128"])
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("shape", SLOW_SHAPES, ids=str)
 def test_long_sequences_full_output(shape, dtype, causal, kernel, knobs):
     # The reference checks the whole output of its long shapes for every dtype
     # (tests/test_attention_fwd.py:110-118); so does this test, on both kernels.
+    if kernel == "pp_blocks" and not causal:
+        pytest.skip("the causal schedule knob does not change a non-causal call")
     print(f"prefill long {shape} {dtype} causal={causal} kernel={kernel}", flush=True)
-    knobs("prefill_pp_min_wg", ROUTES[kernel])
+    set_route(knobs, kernel)
     (q, k, v), oracle = _long_case(shape, dtype, causal)
     out, lse = flash_lab.attention(q, k, v, causal=causal, return_lse=True)
     oracle.check(out, lse)
 
 
+@pytest.mark.parametrize("schedule", ["stream", "blocks"])
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
-def test_headline_shape_sampled_rows(causal):
+def test_headline_shape_sampled_rows(causal, schedule, knobs):
+    if schedule == "blocks":
+        if not causal:
+            pytest.skip("the causal schedule knob does not change a non-causal call")
+        knobs("prefill_causal_stream", 0)
     # (B, H, H_kv, S, D) = (4, 32, 32, 4096, 128) bf16, seeded like the benchmark (q, k, v order),
     # on the 256 sampled rows of the reference's benchmark check (bench/run.py:36, 75-79).
     gen = torch.Generator(device="cuda").manual_seed(0)
