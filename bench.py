@@ -330,7 +330,7 @@ def gpu_window(run, step_ms: float, flush=None, seconds: float = CLOCK_WINDOW_S)
 CPU_LEG_BUDGET_S = 6.0  # timed work per CPU leg, beyond its warmup
 CPU_MIN_REPS = 3
 CPU_MAX_REPS = 10
-CPU_DECODE_REPS = 10  # the decode legs always run this many (median of >= 10 runs)
+CPU_DECODE_REPS = 10  # the decode legs always run this many (a median of at least 10 runs)
 
 
 def time_cpu(fn, budget_s: float = CPU_LEG_BUDGET_S, warmed_up: bool = False,

@@ -13,9 +13,9 @@
 //    Q^T the B operand in registers: one query head per column, columns past the group zero), and
 //    the output as O^T = V^T P^T (V^T read with ds_read_b64_tr_b16). Lane l holds query head
 //    l % 32 and 16 of a tile's 32 keys, so softmax state and output rescaling are per lane.
-//    The online softmax keeps a lazily moved reference point (as prefill_pp.hip does): a tile's
-//    probabilities are taken against it, and only when a lane's sum exceeds 2^15 is the row max
-//    taken and O and l rescaled, so most tiles skip the max and the rescale of O.
+//    The online softmax keeps the running max of each head's scores as its reference point (as
+//    the reference and prefill_pp.hip do); O and l are rescaled only on tiles where some head's
+//    max grows, so most tiles of a long sequence skip the rescale of O.
 //  * Workgroup: 4 waves and one split, in one of two layouts (mfma_span, chosen on the host): one
 //    KV head with all of its query heads (up to 32), wave w taking the split's 32-key tiles w,
 //    w + 4, w + 8, ... (the four waves read neighbouring rows); or four adjacent KV heads, wave w
@@ -63,10 +63,8 @@ constexpr int kTileKeys = 32;  // one MFMA key block
 #endif
 constexpr int kAhead = FL_DMFMA_AHEAD;  // tiles in flight in registers per wave
 constexpr float kLn2 = 0.693147180559945309f;
-// Largest lane sum of a tile's probabilities (16 of them) kept without moving the reference point.
-constexpr float kSumLimit = 32768.f;
-// Reference point before the first tile: finite, so the first tile's probabilities overflow and
-// take the path that moves it, and masked scores (-inf) still give 0.
+// Running max before the first tile: finite, so the first tile's max passes it and masked scores
+// (-inf) still give 0.
 constexpr float kNoRef = -1e30f;
 
 template <int D>
@@ -203,9 +201,9 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
 #pragma unroll
   for (int nb = 0; nb < D / 32; ++nb) o[nb] = f32x16{};
   // Reference point of o and l for the lane's head (log2 units, the same in both halves of a
-  // column; kNoRef until the first tile). Probabilities are 2^(s scale_log2 - ref), and the point
-  // moves only when a lane's sum of them exceeds kSumLimit, so each stays at most 2^15 (fp16
-  // reaches 65504).
+  // column; kNoRef until the first tile): the running max of its scores, as in the reference's
+  // online softmax. Probabilities are 2^(s scale_log2 - ref) <= 1, and the largest key seen so far
+  // has p = 1 exactly, which the rounding of P to the input type keeps exact.
   float ref = kNoRef;
   float l = 0.f;  // the lane's part of the running sum (its 16 keys of each tile)
   const float sl2 = a.scale_log2;
@@ -242,35 +240,28 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
         if (acc_key(j, 0) > lim) s[j] = -INFINITY;
       }
     }
-    // Probabilities against the current reference point; it moves (and O and l are rescaled)
-    // only when a lane's sum exceeds kSumLimit, which the first tile always does (ref starts at
-    // kNoRef). The row max is therefore not needed on most tiles, and O, which the compiler keeps in
-    // accumulator registers, is not touched by VALU work between them.
-    f32x16 p;
-    auto probabilities = [&]() __attribute__((always_inline)) {
-      float r = 0.f;
+    // The running max moves (and O and l are rescaled, a wave-uniform branch) only on tiles where
+    // some head's max grows, so O, which the compiler keeps in accumulator registers, is left
+    // alone on most tiles of a long sequence.
+    float mx = s[0];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        p[j] = exp2_fast(fmaf(s[j], sl2, -ref));
-        r += p[j];
-      }
-      return r;
-    };
-    float rs = probabilities();
-    if (wave_any(rs > kSumLimit)) {
-      float mx = s[0];
-#pragma unroll
-      for (int j = 1; j < 16; ++j) mx = fmaxf(mx, s[j]);
-      // scale_log2 > 0, so the max commutes with it; every row sees a valid key of the tile.
-      const float moved = fmaxf(ref, max_halves(mx) * sl2);
+    for (int j = 1; j < 16; ++j) mx = fmaxf(mx, s[j]);
+    // scale_log2 > 0, so the max commutes with it; every column sees a valid key of the tile.
+    mx = max_halves(mx) * sl2;
+    if (wave_any(mx > ref)) {
+      const float moved = fmaxf(ref, mx);
       const float alpha = exp2_fast(ref - moved);  // 0 on the first tile
       ref = moved;
-      if (wave_any(alpha != 1.f)) {
 #pragma unroll
-        for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
-      }
+      for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
       l *= alpha;
-      rs = probabilities();
+    }
+    f32x16 p;
+    float rs = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      p[j] = exp2_fast(fmaf(s[j], sl2, -ref));
+      rs += p[j];
     }
     l += rs;
     const u32x4 p0 = p_frag<Tag, 0>(p);

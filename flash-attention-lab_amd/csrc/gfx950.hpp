@@ -176,11 +176,18 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// Maxes the compiler turns into v_max_f32 / v_max3_f32. (Not inline assembly: an asm statement
+// that reads an MFMA result is invisible to the compiler's wait-state insertion for the
+// MFMA -> VALU read hazard. Operands the compiler cannot prove quiet, e.g. masked selects, get a
+// self-max for IEEE-mode NaN quieting first; MFMA results need none.)
+__device__ __forceinline__ float max2_f32(float a, float b) { return fmaxf(a, b); }
+__device__ __forceinline__ float max3_f32(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+
 // max(x[l], x[l ^ 32]) and x[l] + x[l ^ 32] on every lane: one v_permlane32_swap (lanes 32-63 of
 // the first result and lanes 0-31 of the second are the other half's values).
 __device__ __forceinline__ float max_halves(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max2_f32(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float sum_halves(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);

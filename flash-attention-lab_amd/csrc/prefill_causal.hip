@@ -325,12 +325,15 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   // of the unrounded probabilities.
   auto probabilities = [&](float neg_shift) -> float {
     f32x16 p0, p1;
-    float r0 = 0.f;
-    float r1 = 0.f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       p0[j] = exp2_fast(fmaf(s0[j], sl2, neg_shift));
       p1[j] = exp2_fast(fmaf(s1[j], sl2, neg_shift));
+    }
+    float r0 = p0[0];  // (not 0 + p: the compiler keeps that add, for -0)
+    float r1 = p1[0];
+#pragma unroll
+    for (int j = 1; j < 16; ++j) {
       r0 += p0[j];
       r1 += p1[j];
     }
@@ -340,8 +343,8 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     pf[3] = p_frag<Tag, 1>(p1);
     return r0 + r1;
   };
-  // Softmax of key tile t for the rows the wave is on, with the lazily moved reference point of
-  // prefill_pp.hip: the max / rescale path runs only when a lane's sum exceeds kSumLimit.
+  // Softmax of key tile t for the rows the wave is on, with the reference point of prefill_pp.hip
+  // (moved to the running max when a tile's max passes it by more than kMoveSlack).
   auto softmax_phase = [&](int t) {
 #if FL_PP_SETPRIO == 2
     __builtin_amdgcn_s_setprio(1);
@@ -357,20 +360,17 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    float rs = probabilities(-ref);
-    if (wave_any(rs > kSumLimit)) {
+    const float mx = max_halves(max_of(s0, s1)) * sl2;
+    if (wave_any(mx > ref + kMoveSlack)) {
       asm volatile("" ::: "memory");
-      const float moved = fmaxf(ref, max_halves(max_of(s0, s1)) * sl2);
+      const float moved = max2_f32(ref, mx);
       const float alpha = exp2_fast(ref - moved);
       ref = moved;
-      if (wave_any(alpha != 1.f)) {
 #pragma unroll
-        for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
-      }
+      for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
       l *= alpha;
-      rs = probabilities(-ref);
     }
-    l += rs;
+    l += probabilities(-ref);
 #if FL_PP_SETPRIO == 2
     __builtin_amdgcn_s_setprio(0);
 #endif
@@ -457,24 +457,32 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   // Periods 0 .. stream, one barrier each. Group 0: MFMA(p), then the softmax of tile p. Group 1:
   // the softmax of tile p - 1, then MFMA(p). Group 0 loads K(p + kStages - 1) and group 1
   // V(p + kStages - 2) between the MFMAs of their phases. A wave's periods come in segments, each
-  // with its own MFMA phase (so every segment is straight-line code):
+  // with its own MFMA phase and events fixed at compile time (so every segment is straight-line
+  // code):
   //  * light: K Q^T only (period 0), then full periods; after the last light K Q^T the heavy query
   //    rows are loaded;
   //  * switch: the P V of the last light tile and the light rows' output, idle periods (loads
   //    only), the first heavy K Q^T; or, with no idle period, one full period that does the P V of
   //    the last light tile and the K Q^T of the first heavy one with the output in between;
   //  * heavy: full periods, then the P V of the last heavy tile.
+  // The heavy query rows are consumed (the compiler's wait for them) at a fixed point of each
+  // switch path, before any loop: the compiler cannot see the tile loads, so a wait it had to
+  // place inside a loop for loads that might still be in flight would drain the whole tile
+  // pipeline every period. The loops also use the plain period-end wait; the first two heavy
+  // periods, which the switch's extra memory instructions may still precede, use the counted one.
   using kFirstT = std::integral_constant<int, 0>;
   using kFullT = std::integral_constant<int, 1>;
   using kLastT = std::integral_constant<int, 2>;
   using kLoadsT = std::integral_constant<int, 3>;
+  using T = std::true_type;
+  using F = std::false_type;
   auto run = [&](auto group_tag) {
     constexpr int kGroup = decltype(group_tag)::value;
     constexpr int kLead = kGroup == 0 ? kStages - 1 : kStages - 2;
-    // After its MFMA phase a period may load the heavy query rows (q_load) and / or write the
-    // light rows and switch to the heavy ones (to_heavy); q_wait consumes the heavy query rows at
-    // its start.
-    auto period = [&](int p, auto mode_tag, bool q_wait, bool q_load, bool to_heavy) {
+    // Event flags (compile-time): q_wait consumes the heavy query rows at the period's start;
+    // q_load loads them after its MFMA phase; to_heavy writes the light rows and switches to the
+    // heavy ones after its MFMA phase; counted selects the period-end wait that counts them.
+    auto period = [&](int p, auto mode_tag, auto q_wait, auto q_load, auto to_heavy, auto counted) {
       constexpr int kMode = decltype(mode_tag)::value;
       constexpr bool kDoPv = kMode == kFullT::value || kMode == kLastT::value;
       constexpr bool kDoQk = kMode == kFirstT::value || kMode == kFullT::value;
@@ -495,10 +503,10 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
         }
       };
       auto after_mfma = [&]() {
-        if (q_load) load_q(heavy.row0);
-        if (to_heavy) switch_to_heavy();
+        if constexpr (decltype(q_load)::value) load_q(heavy.row0);
+        if constexpr (decltype(to_heavy)::value) switch_to_heavy();
       };
-      if (q_wait) consume_q();
+      if constexpr (decltype(q_wait)::value) consume_q();
       if constexpr (kMode == kFirstT::value) prefetch_qk(slot);
       if constexpr (kGroup == 0) {
         mfma();
@@ -519,48 +527,75 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
         operands_dead();
         after_mfma();
       }
-      period_end_wait(p, group_tag);
+      if constexpr (decltype(counted)::value) {
+        period_end_wait(p, group_tag);
+      } else {
+        wait_vmcnt<kGroup == 0 ? kPendingK : kPendingV>();
+      }
       phase_barrier();
     };
-    const bool f = false;
     int m = 0;
-    // Light part: K Q^T of tiles 0 .. light.tiles - 1 (each P V one period later).
-    if (light.tiles > 0) {
-      period(0, kFirstT{}, f, q_switch && light.tiles == 1, f);
-      for (m = 1; m < light.tiles - 1; ++m) period(m, kFullT{}, f, f, f);
-      if (light.tiles > 1) period(m, kFullT{}, f, q_switch, f);
-      m = light.tiles;
+    // Light part: K Q^T of tiles 0 .. light.tiles - 1 (each P V one period later). The period
+    // after which the heavy query rows load is its own instance, so no loop sees them in flight.
+    if (light.tiles == 1) {
+      if (q_switch) {
+        period(0, kFirstT{}, F{}, T{}, F{}, T{});
+      } else {
+        period(0, kFirstT{}, F{}, F{}, F{}, T{});
+      }
+    } else if (light.tiles > 1) {
+      period(0, kFirstT{}, F{}, F{}, F{}, F{});
+      for (m = 1; m < light.tiles - 1; ++m) period(m, kFullT{}, F{}, F{}, F{}, F{});
+      if (q_switch) {
+        period(m, kFullT{}, F{}, T{}, F{}, T{});
+      } else {
+        period(m, kFullT{}, F{}, F{}, F{}, T{});
+      }
     }
+    m = light.tiles;
     if (!two) {
       if (light.tiles > 0) {
-        period(m, kLastT{}, f, f, f);
+        period(m, kLastT{}, F{}, F{}, F{}, T{});
         ++m;
       }
-      for (; m <= stream; ++m) period(m, kLoadsT{}, f, f, f);
+      for (; m <= stream; ++m) period(m, kLoadsT{}, F{}, F{}, F{}, T{});
       return;
     }
-    // Switch (a wave without light tiles wrote its light rows, as zeros, before period 0).
-    if (light.tiles > 0 && heavy.tiles > 0 && heavy_start == light.tiles) {
-      period(m, kFullT{}, m == q_consume, f, true);
-      ++m;
-    } else {
+    // Switch. Without light tiles the wave wrote its light rows (as zeros) before period 0 and
+    // loaded its heavy query rows in the prologue.
+    if (!q_switch) {
       if (light.tiles > 0) {
-        period(m, kLastT{}, m == q_consume, f, true);
+        period(m, kLastT{}, F{}, F{}, T{}, T{});
         ++m;
       }
-      for (; m < heavy_start; ++m) period(m, kLoadsT{}, m == q_consume, f, f);
+      for (; m < heavy_start; ++m) period(m, kLoadsT{}, F{}, F{}, F{}, T{});
       if (heavy.tiles > 0) {
-        period(m, kFirstT{}, m == q_consume, f, f);
+        period(m, kFirstT{}, F{}, F{}, F{}, T{});
         ++m;
       }
+    } else if (heavy_start == light.tiles) {
+      // No idle period: the query rows are consumed at the start of this one.
+      period(m, kFullT{}, T{}, F{}, T{}, T{});
+      ++m;
+    } else if (heavy_start == light.tiles + 1) {
+      period(m, kLastT{}, T{}, F{}, T{}, T{});
+      period(m + 1, kFirstT{}, F{}, F{}, F{}, T{});
+      m += 2;
+    } else {
+      period(m, kLastT{}, F{}, F{}, T{}, T{});
+      for (++m; m < heavy_start - 1; ++m) period(m, kLoadsT{}, F{}, F{}, F{}, T{});
+      period(m, kLoadsT{}, T{}, F{}, F{}, T{});  // the last idle period: consume the query rows
+      period(m + 1, kFirstT{}, F{}, F{}, F{}, T{});
+      m += 2;
     }
     // Heavy part: full periods up to the last heavy K Q^T (period stream - 1), then its P V.
     if (heavy.tiles > 0) {
-      for (; m < stream; ++m) period(m, kFullT{}, f, f, f);
-      period(m, kLastT{}, f, f, f);
+      for (int i = 0; i < 2 && m < stream; ++i, ++m) period(m, kFullT{}, F{}, F{}, F{}, T{});
+      for (; m < stream; ++m) period(m, kFullT{}, F{}, F{}, F{}, F{});
+      period(m, kLastT{}, F{}, F{}, F{}, T{});
       ++m;
     }
-    for (; m <= stream; ++m) period(m, kLoadsT{}, f, f, f);
+    for (; m <= stream; ++m) period(m, kLoadsT{}, F{}, F{}, F{}, T{});
   };
   if (group == 0) {
     run(std::integral_constant<int, 0>{});

@@ -26,23 +26,6 @@ namespace {
 
 constexpr int kXcds = 8;
 constexpr float kLn2 = 0.693147180559945309f;
-// log2 of the largest probability the lazily moved reference point allows.
-constexpr float kRescaleSlack = 8.f;
-
-// Max of the 32 scores a lane holds, as a tree of three-input maxes.
-__device__ __forceinline__ float max_of(const f32x16& x, const f32x16& y) {
-  float t[11];
-#pragma unroll
-  for (int i = 0; i < 5; ++i) t[i] = fmaxf(fmaxf(x[3 * i], x[3 * i + 1]), x[3 * i + 2]);
-#pragma unroll
-  for (int i = 0; i < 5; ++i) t[5 + i] = fmaxf(fmaxf(y[3 * i], y[3 * i + 1]), y[3 * i + 2]);
-  t[10] = fmaxf(x[15], y[15]);
-  const float u0 = fmaxf(fmaxf(t[0], t[1]), t[2]);
-  const float u1 = fmaxf(fmaxf(t[3], t[4]), t[5]);
-  const float u2 = fmaxf(fmaxf(t[6], t[7]), t[8]);
-  const float u3 = fmaxf(t[9], t[10]);
-  return fmaxf(fmaxf(u0, u1), fmaxf(u2, u3));
-}
 
 // Bijection on [0, n): ids dealt to XCD x (id % 8 == x) get the contiguous range
 // [x * n / 8, (x + 1) * n / 8) of work items. A ragged tail keeps its own ids.
@@ -232,13 +215,13 @@ __global__ void __launch_bounds__(kThreads)
       }
       // Online softmax in the exp2 domain on raw scores: with scale > 0,
       // max(scale * s) = scale * max(s), and p = 2^(s * scale_log2 - ref). The reference point
-      // `ref` of o and l only moves when the row max has grown by more than kRescaleSlack over
-      // it, so probabilities stay at most 2^kRescaleSlack (no overflow; a bf16/fp16 P keeps its
-      // relative precision) and most tiles skip the rescale of o.
+      // `ref` of o and l moves to the row's running max when it has grown by more than
+      // kMoveSlack over it (prefill_tile.hpp), so probabilities stay at most 2^kMoveSlack and most
+      // tiles of a long row skip the rescale of o.
       float mx = max_of(s0, s1);
-      mx = fmaxf(mx, xor_lane(mx, 32));
+      mx = max2_f32(mx, xor_lane(mx, 32));
       const float cand = mx * sl2;  // -inf while the row has seen only hidden keys
-      const bool move = cand > ref + kRescaleSlack;
+      const bool move = cand > ref + kMoveSlack;
       const float alpha = move ? exp2_fast(ref - cand) : 1.f;  // ref = -inf gives 0
       ref = move ? cand : ref;
       if (wave_any(move)) {

@@ -209,22 +209,41 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     const float sl2 = a.scale_log2;
     const int last_key = a.causal ? min(a.seqlen_k - 1, my_row + a.causal_offset) : a.seqlen_k - 1;
 
-    // MFMA phase of a period with slots kS = m % kStages: O += V(m-1) P(m-1) (16 MFMAs), then
+    // MFMA phase of a period with slots kS = m % kStages: O += V(m-1) P(m-1) (16 MFMAs) and
     // S = K(m) Q^T (16 MFMAs). No branches: in period 0 the previous P and V are zeros (P starts at
     // 0, the V slot was filled from an empty resource), a skipped softmax leaves P = 0, and scores of
     // tiles nobody reads are never used. The 32 MFMAs form one software pipeline: the A-operand
-    // fragment of MFMA i + kAhead is read from LDS right after MFMA i issues, and a scheduling
-    // barrier after every step keeps that order (left to itself the scheduler reads each fragment
-    // just before its MFMA and the LDS latency shows on every step). The first kAhead fragments are
-    // read at the end of the wave's softmax phase (prefetch), so the MFMA phase starts without
-    // waiting for LDS. hook(i) runs after MFMA i (the tile loads are issued there).
+    // fragment of the MFMA kAhead steps later is read from LDS right after an MFMA issues, and a
+    // scheduling barrier after every step keeps that order (left to itself the scheduler reads each
+    // fragment just before its MFMA and the LDS latency shows on every step). The first kAhead
+    // fragments are read at the end of the wave's softmax phase (prefetch), so the MFMA phase
+    // starts without waiting for LDS. hook(i) runs after the MFMA of phase step i (the tile loads
+    // are issued there).
+    // A phase with both parts runs the first kLeadPv P V steps, then K Q^T, then the rest of P V,
+    // and computes the tile's row max (tile_mx, for the softmax that follows) between those last
+    // P V MFMAs, from the scores K Q^T has just completed: the max tree then takes issue slots the
+    // MFMA wave has free instead of lengthening the softmax phase, which sets the half-period. The
+    // lead steps cover the latency of the first K fragment reads (K(m) is published by the barrier
+    // that starts the phase, so its fragments cannot be prefetched).
     constexpr int kPv = 4 * (D / 32);  // P V MFMAs: key step kk = i / (D / 32), dim block nb
     constexpr int kQk = 2 * (D / 16);  // K Q^T MFMAs: dim step ks = j / 2, key block j % 2
     constexpr int kSteps = kPv + kQk;
     constexpr int kAhead = FL_PP_AHEAD;
-    static_assert(kAhead >= 1 && kAhead <= kPv, "prefetched fragments are V fragments");
+    constexpr int kLeadPv = kPv - 4;
+    constexpr int kTail = kPv - kLeadPv;  // P V steps after K Q^T
+    static_assert(kAhead >= 1 && kAhead <= kLeadPv, "prefetched fragments are V fragments");
+    static_assert(kTail >= 2, "room for the max tree");
     static_assert(8 * (kDmaPerWave - 1) + 1 < kSteps, "one tile load every 8 MFMAs");
-    // Fragment of MFMA i of the phase with slots kS = m % kStages: V(m - 1) sits in V slot
+    // Logical step (i < kPv: P V step i; else K Q^T step i - kPv) of phase position n.
+    auto step_at = [](auto n_tag, auto full_tag) constexpr {
+      constexpr int n = decltype(n_tag)::value;
+      if constexpr (!decltype(full_tag)::value) {
+        return n;
+      } else {
+        return n < kLeadPv ? n : n < kLeadPv + kQk ? kPv + (n - kLeadPv) : n - kQk;
+      }
+    };
+    // Fragment of logical step i of the phase with slots kS = m % kStages: V(m - 1) sits in V slot
     // kS + kStages - 1, K(m) in K slot kS.
     auto read_frag = [&](int slot, auto i_tag) -> u32x4 {
       constexpr int i = decltype(i_tag)::value;
@@ -250,12 +269,44 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
         pre[decltype(i)::value] = read_frag(slot, std::integral_constant<int, kPv + decltype(i)::value>{});
       });
     };
+    // Row max of the scores (log2 units, both halves of the row), computed by the MFMA phase that
+    // produced them; the softmax of a masked tile computes its own.
+    float tile_mx = kNoRef;
+    float mx_t[10], mx_u[4], mx_w = 0.f;
+    // Op k of the max tree over s0, s1 (18 ops: s0's leaves first, whose MFMAs finish first).
+    auto max_op = [&](auto k_tag) {
+      constexpr int k = decltype(k_tag)::value;
+      if constexpr (k < 5) {
+        mx_t[k] = max3_f32(s0[3 * k], s0[3 * k + 1], s0[3 * k + 2]);
+      } else if constexpr (k < 10) {
+        mx_t[k] = max3_f32(s1[3 * (k - 5)], s1[3 * (k - 5) + 1], s1[3 * (k - 5) + 2]);
+      } else if constexpr (k < 13) {
+        mx_u[k - 10] = max3_f32(mx_t[3 * (k - 10)], mx_t[3 * (k - 10) + 1], mx_t[3 * (k - 10) + 2]);
+      } else if constexpr (k == 13) {
+        mx_u[3] = max3_f32(mx_t[9], s0[15], s1[15]);
+      } else if constexpr (k == 14) {
+        mx_w = max3_f32(mx_u[0], mx_u[1], mx_u[2]);
+      } else if constexpr (k == 15) {
+        mx_w = max2_f32(mx_w, mx_u[3]);
+      } else if constexpr (k == 16) {
+        mx_w = max_halves(mx_w);
+      } else {
+        tile_mx = mx_w * sl2;  // scale_log2 > 0, so the max commutes with it
+      }
+    };
+    constexpr int kMaxOps = 18;
     auto mfma_phase = [&](int slot, auto pv_tag, auto qk_tag, auto&& hook) {
       constexpr bool kDoPv = decltype(pv_tag)::value;
       constexpr bool kDoQk = decltype(qk_tag)::value;
-      constexpr int kFirstStep = kDoPv ? 0 : kPv;
-      u32x4 fr[kSteps];
-      static_for<0, kAhead>([&](auto i) { fr[kFirstStep + decltype(i)::value] = pre[decltype(i)::value]; });
+      constexpr bool kFull = kDoPv && kDoQk;
+      // Live phase positions are [kFirstLive, kEndLive); the first kAhead of them were prefetched.
+      constexpr int kFirstLive = kDoPv ? 0 : kPv;
+      constexpr int kEndLive = kDoQk ? kSteps : kPv;
+      u32x4 fr[kSteps];  // by logical step
+      static_for<0, kAhead>([&](auto i) {
+        constexpr int n = kFirstLive + decltype(i)::value;
+        fr[step_at(std::integral_constant<int, n>{}, std::bool_constant<kFull>{})] = pre[decltype(i)::value];
+      });
       auto issue = [&](auto i_tag, const u32x4& f) {
         constexpr int i = decltype(i_tag)::value;
         if constexpr (i < kPv) {
@@ -271,20 +322,27 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
       __builtin_amdgcn_s_setprio(1);
 #endif
       __builtin_amdgcn_sched_barrier(0);
-      static_for<0, kSteps>([&](auto i) {
-        constexpr int n = decltype(i)::value;
-        constexpr bool kLive = n < kPv ? kDoPv : kDoQk;
-        if constexpr (kLive) issue(i, fr[n]);
-        // Read ahead only the fragments of live steps (a K Q^T-only phase has them prefetched).
-        if constexpr (n + kAhead < kSteps && (n + kAhead < kPv ? kDoPv : (kDoQk && (kDoPv || n >= kPv)))) {
-          fr[n + kAhead] = read_frag(slot, std::integral_constant<int, n + kAhead>{});
+      static_for<0, kSteps>([&](auto n_tag) {
+        constexpr int n = decltype(n_tag)::value;
+        constexpr int i = step_at(n_tag, std::bool_constant<kFull>{});
+        if constexpr (n >= kFirstLive && n < kEndLive) issue(std::integral_constant<int, i>{}, fr[i]);
+        constexpr int nx = n + kAhead;
+        if constexpr (nx >= kFirstLive + kAhead && nx < kEndLive) {
+          constexpr int ix = step_at(std::integral_constant<int, nx>{}, std::bool_constant<kFull>{});
+          fr[ix] = read_frag(slot, std::integral_constant<int, ix>{});
         }
-        hook(i);
+        hook(n_tag);
+        if constexpr (kFull && n >= kLeadPv + kQk) {
+          constexpr int k = n - (kLeadPv + kQk);
+          static_for<k * kMaxOps / kTail, (k + 1) * kMaxOps / kTail>([&](auto op) { max_op(op); });
+        }
         __builtin_amdgcn_sched_barrier(0);
       });
 #if FL_PP_SETPRIO == 1
       __builtin_amdgcn_s_setprio(0);
 #endif
+      // A K Q^T-only phase (tile 0) has no P V MFMAs to hide the tree behind.
+      if constexpr (kDoQk && !kDoPv) static_for<0, kMaxOps>([&](auto op) { max_op(op); });
     };
     // A phase whose MFMAs nobody in the group needs (causal tiles past the diagonal of all of the
     // group's rows): only its tile loads.
@@ -298,12 +356,15 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     // other wave's MFMAs, which more than doubles the phase).
     auto probabilities = [&](float neg_shift) -> float {
       f32x16 p0, p1;
-      float r0 = 0.f;
-      float r1 = 0.f;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         p0[j] = exp2_fast(fmaf(s0[j], sl2, neg_shift));
         p1[j] = exp2_fast(fmaf(s1[j], sl2, neg_shift));
+      }
+      float r0 = p0[0];  // (not 0 + p: the compiler keeps that add, for -0)
+      float r1 = p1[0];
+#pragma unroll
+      for (int j = 1; j < 16; ++j) {
         r0 += p0[j];
         r1 += p1[j];
       }
@@ -315,15 +376,14 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     };
 
     // Softmax phase for tile t: S(t) -> P(t) and the running sum. The reference point `ref` (log2
-    // units, the same for both halves of a row) only moves when it must: the probabilities are first
-    // computed against the current one, and only if a lane's sum exceeds kSumLimit (so some p might
-    // leave the comfortable range of the packed operand; fp16 tops out at 65504) does the wave take
-    // the max / rescale path and recompute them. A row without a reference yet (kNoRef) overflows
-    // on its first tile with a visible key. The row max is therefore not needed on most tiles, and
-    // every probability stays <= kSumLimit.
+    // units, the same for both halves of a row) moves to the row's running max when the tile's max
+    // passes it by more than kMoveSlack (a wave-uniform branch: the rescale of o runs only on tiles
+    // where some row of the wave moved). A row without a key yet keeps kNoRef, so its masked scores
+    // give p = 0.
     // It runs only for tiles t < my_tiles: a wave's periods past its last visible tile are
     // loads-only.
     auto softmax_body = [&](int t) {
+      float mx = tile_mx;
       if (t >= mask_from) {
         asm volatile("" ::: "memory");
         // acc_key(j, half) = acc_key(j, 0) + 4 half: fold the lane's part into the limit so every
@@ -340,21 +400,18 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
           // 86 scalar registers (reloaded on every masked tile).
           __builtin_amdgcn_sched_barrier(0);
         }
+        mx = max_halves(max_of(s0, s1)) * sl2;  // -inf for a tile the row sees no key of
       }
-      float rs = probabilities(-ref);
-      if (wave_any(rs > kSumLimit)) {
+      if (wave_any(mx > ref + kMoveSlack)) {
         asm volatile("" ::: "memory");
-        const float moved = fmaxf(ref, max_halves(max_of(s0, s1)) * sl2);
-        const float alpha = exp2_fast(ref - moved);
+        const float moved = max2_f32(ref, mx);
+        const float alpha = exp2_fast(ref - moved);  // 0 for a row's first key (ref = kNoRef)
         ref = moved;
-        if (wave_any(alpha != 1.f)) {
 #pragma unroll
-          for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
-        }
+        for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
         l *= alpha;
-        rs = probabilities(-ref);
       }
-      l += rs;
+      l += probabilities(-ref);
     };
     auto softmax_phase = [&](int t) {
 #if FL_PP_SETPRIO == 2
@@ -564,7 +621,7 @@ hipError_t launch_typed(PrefillArgs args, hipStream_t stream) {
 hipError_t launch_prefill_pingpong(const PrefillArgs& args, DType dtype, int head_dim,
                                    hipStream_t stream) {
   using namespace prefill::pp;
-  if (args.causal && knob(FL_KNOB_PREFILL_CAUSAL_STREAM) != 0)
+  if (args.causal && knob(FL_KNOB_PREFILL_CAUSAL_STREAM) == 1)
     return launch_prefill_causal_stream(args, dtype, head_dim, stream);
   if (head_dim == 64) {
     return dtype == DType::bf16 ? launch_typed<bf16_tag, 64>(args, stream)

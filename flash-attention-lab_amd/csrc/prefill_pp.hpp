@@ -20,11 +20,9 @@ constexpr int kPpBlockM = kRowsPerWave * kPpWaves;  // 256 query rows per workgr
 constexpr int kLoadWaves = 4;                       // waves per group: one group per tensor
 constexpr int kXcds = 8;
 constexpr float kLn2 = 0.693147180559945309f;
-// Largest lane sum of probabilities (32 of them) kept without moving the reference point.
-constexpr float kSumLimit = 32768.f;
-// Reference point of a row that has not seen a score yet: finite, so p = 2^(s scale_log2 - ref)
-// overflows (sum above kSumLimit: the first tile with a key takes the max path) and masked scores
-// still give 0, with no separate test for "no reference yet".
+// Reference point of a row that has not seen a key yet: finite, so a masked score (-inf) still
+// gives p = 2^(s scale_log2 - ref) = 0 and the first visible key always moves it, with no separate
+// test for "no key yet".
 constexpr float kNoRef = -1e30f;
 
 // LDS ring depth (K and V slots each). A K tile is issued kStages - 1 periods before the period
@@ -44,20 +42,6 @@ static_assert(kStages == 3 || kStages == 4, "3 or 4 ring stages");
 #ifndef FL_PP_AHEAD
 #define FL_PP_AHEAD 2
 #endif
-
-__device__ __forceinline__ float max_of(const f32x16& x, const f32x16& y) {
-  float t[11];
-#pragma unroll
-  for (int i = 0; i < 5; ++i) t[i] = fmaxf(fmaxf(x[3 * i], x[3 * i + 1]), x[3 * i + 2]);
-#pragma unroll
-  for (int i = 0; i < 5; ++i) t[5 + i] = fmaxf(fmaxf(y[3 * i], y[3 * i + 1]), y[3 * i + 2]);
-  t[10] = fmaxf(x[15], y[15]);
-  const float u0 = fmaxf(fmaxf(t[0], t[1]), t[2]);
-  const float u1 = fmaxf(fmaxf(t[3], t[4]), t[5]);
-  const float u2 = fmaxf(fmaxf(t[6], t[7]), t[8]);
-  const float u3 = fmaxf(t[9], t[10]);
-  return fmaxf(fmaxf(u0, u1), fmaxf(u2, u3));
-}
 
 __device__ __forceinline__ int xcd_remap(int id, int n) {
   const int per = n / kXcds;

@@ -113,4 +113,39 @@ __device__ __forceinline__ constexpr int acc_key(int j, int half) {
   return 8 * (j >> 2) + 4 * half + (j & 3);
 }
 
+// Online softmax reference point of a row (log2 units; o and l are kept relative to it): it moves
+// to the row's running max when a tile's max passes it by more than kMoveSlack, so every
+// probability is at most 2^kMoveSlack, and the key that set it has p = 1 exactly. What this
+// trades: a key's p is rounded to the input type (2^-8 relative in bf16) unless it is exactly a
+// power of two, and the reference's exact running max keeps the largest key of a row at p = 1,
+// exact, whatever its share of the row. A point that moved only when a lane's probabilities summed
+// past 2^15 left a dominant key that arrives after the point at p >> 1 and rounded; on a row where
+// one key holds 16% of the weight that was 1.8e-3 of error before the output rounding, against
+// 2.5e-4 with the exact max, and broke the reference's tolerance. With a slack of 3 a key stays
+// rounded only while it is within 8x of the weight of the exact key that set the point, and a key
+// that dominates its row moves it. In CPU emulations of this arithmetic (randn inputs at three
+// score scales, and rows with a planted dominant key at a random position) slacks 0 to 3 gave the
+// exact max's error to within 10% and the 2^15 rule up to 1.7x of it. Cost against the 2^15 rule,
+// headline shape: slack 0 (the exact max: a new max in any of a wave's 32 rows on 42 of 64 tiles,
+// each a 64-multiply rescale of o, and the workgroup barrier makes every wave wait for the
+// slowest) -17%; slack 1 -8% / -12% (non-causal / causal); 2 -4% / -6%; 3 -3.5% / -3%.
+constexpr float kMoveSlack = 3.f;
+
+// Max of the 32 scores a lane holds (a tile's 64 keys of its row, split with the other half),
+// as 16 three-input maxes.
+__device__ __forceinline__ float max_of(const f32x16& x, const f32x16& y) {
+  float t[12];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) t[i] = max3_f32(x[3 * i], x[3 * i + 1], x[3 * i + 2]);
+#pragma unroll
+  for (int i = 0; i < 5; ++i) t[5 + i] = max3_f32(y[3 * i], y[3 * i + 1], y[3 * i + 2]);
+  t[10] = x[15];
+  t[11] = y[15];
+  const float u0 = max3_f32(t[0], t[1], t[2]);
+  const float u1 = max3_f32(t[3], t[4], t[5]);
+  const float u2 = max3_f32(t[6], t[7], t[8]);
+  const float u3 = max3_f32(t[9], t[10], t[11]);
+  return max2_f32(max3_f32(u0, u1, u2), u3);
+}
+
 }  // namespace fl::prefill

@@ -187,9 +187,10 @@ int fl_mfma_tile_test(const void* a, const void* b, float* c, int32_t k, int32_t
  *                                  values act as 1), whatever the size of
  *                                  the call.
  *   FL_KNOB_PREFILL_CAUSAL_STREAM  [0, 1]: how the 8-wave kernel runs a
- *                                  causal pair of query blocks: 1 = one
- *                                  stream of key tiles (the default), 0 = two
- *                                  blocks one after the other.
+ *                                  causal pair of query blocks: 0 = two
+ *                                  blocks one after the other (the default),
+ *                                  1 = one stream of key tiles (measured
+ *                                  slower; kept for comparison).
  */
 enum fl_knob {
   FL_KNOB_PREFILL_PP_MIN_WG = 0,

@@ -64,12 +64,12 @@ def sampled_rows(seqlen, count, seed=0):
 # The library runs the 8-wave ping-pong kernel when it fills at least 256 workgroups and the
 # 4-wave kernel below that (head_dim 64 and 128 alike); the prefill_pp_min_wg knob routes a shape
 # to either one, so both are checked on every shape. The ping-pong kernel runs a causal pair of
-# query blocks as one stream of key tiles (prefill_causal.hip, the default) or as two blocks
-# (prefill_pp.hip, the prefill_causal_stream knob at 0): "pp_blocks" checks the second.
+# query blocks as two blocks (prefill_pp.hip, the default) or as one stream of key tiles
+# (prefill_causal.hip, the prefill_causal_stream knob at 1): "pp_stream" checks the second.
 ROUTES = {
     "auto": {},
     "pingpong": {"prefill_pp_min_wg": 0},
-    "pp_blocks": {"prefill_pp_min_wg": 0, "prefill_causal_stream": 0},
+    "pp_stream": {"prefill_pp_min_wg": 0, "prefill_causal_stream": 1},
     "wg128": {"prefill_pp_min_wg": 1 << 30},
 }
 
@@ -113,14 +113,14 @@ def _long_case(shape, dtype, causal):
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("kernel", ["pingpong", "pp_blocks", "wg128"])
+@pytest.mark.parametrize("kernel", ["pingpong", "pp_stream", "wg128"])
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("shape", SLOW_SHAPES, ids=str)
 def test_long_sequences_full_output(shape, dtype, causal, kernel, knobs):
     # The reference checks the whole output of its long shapes for every dtype
     # (tests/test_attention_fwd.py:110-118); so does this test, on both kernels.
-    if kernel == "pp_blocks" and not causal:
+    if kernel == "pp_stream" and not causal:
         pytest.skip("the causal schedule knob does not change a non-causal call")
     print(f"prefill long {shape} {dtype} causal={causal} kernel={kernel}", flush=True)
     set_route(knobs, kernel)
@@ -132,10 +132,10 @@ def test_long_sequences_full_output(shape, dtype, causal, kernel, knobs):
 @pytest.mark.parametrize("schedule", ["stream", "blocks"])
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 def test_headline_shape_sampled_rows(causal, schedule, knobs):
-    if schedule == "blocks":
+    if schedule == "stream":
         if not causal:
             pytest.skip("the causal schedule knob does not change a non-causal call")
-        knobs("prefill_causal_stream", 0)
+        knobs("prefill_causal_stream", 1)
     # (B, H, H_kv, S, D) = (4, 32, 32, 4096, 128) bf16, seeded like the benchmark (q, k, v order),
     # on the 256 sampled rows of the reference's benchmark check (bench/run.py:36, 75-79).
     gen = torch.Generator(device="cuda").manual_seed(0)
