@@ -365,8 +365,8 @@ static_assert(kPrefillBlockN == prefill::kBlockN, "host and kernel tile widths d
 #define FL_PREFILL_PINGPONG 1
 #endif
 
-// Below this many ping-pong workgroups (256 query rows each, causal blocks paired; one per CU) a
-// problem runs on this kernel instead, whose 128-row workgroups (two per CU) spread a
+// Below this many ping-pong workgroups (256 query rows each at head_dim 128, 384 at 64; causal
+// blocks paired; one per CU) a problem runs on this kernel instead, whose 128-row workgroups (two per CU) spread a
 // short prompt over more CUs. Measured on MI355X at B=1, H=32, causal: S=1024 takes 24.6 us here
 // against 42.7 us on the ping-pong kernel (64 workgroups), S=2048 ties, S=4096 (256 ping-pong
 // workgroups) is 128 us there against 161 us here. The FL_KNOB_PREFILL_PP_MIN_WG knob overrides it
@@ -379,7 +379,8 @@ int prefill_pp_min_workgroups() {
 hipError_t launch_prefill(const PrefillArgs& args, DType dtype, int head_dim, hipStream_t stream) {
   using namespace prefill;
   if (FL_PREFILL_PINGPONG) {
-    const int64_t pp_blocks = (args.seqlen_q + 255) / 256;
+    const int rows = prefill_pp_block_rows(head_dim);
+    const int64_t pp_blocks = (args.seqlen_q + rows - 1) / rows;
     const int64_t pp_items = args.causal ? (pp_blocks + 1) / 2 : pp_blocks;
     if (pp_items * args.batch * args.heads >= prefill_pp_min_workgroups())
       return launch_prefill_pingpong(args, dtype, head_dim, stream);

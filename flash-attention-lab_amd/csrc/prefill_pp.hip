@@ -47,9 +47,11 @@ namespace pp {
 namespace {
 
 template <typename Tag, int D>
-__global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
-    prefill_pp_kernel(const PrefillArgs a) {
+__global__ void __launch_bounds__(64 * kPpWavesOf<D>)
+    __attribute__((amdgpu_waves_per_eu(kPpGroups<D>, kPpGroups<D>))) prefill_pp_kernel(const PrefillArgs a) {
   using E = Elem<Tag>;
+  constexpr int kGroups = kPpGroups<D>;
+  constexpr int kBlockM = kPpBlockMOf<D>;
   constexpr int kTile = kTileElems<D>;
   // One LDS array: the K ring (kStages slots) then the V ring. ds_read immediates reach 64 KiB, so
   // V reads go through per-lane offsets biased by the K ring's size and every slot offset is an
@@ -125,7 +127,7 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   // qb kPpBlockM + 32 wave + r, dims 16 ks + 8 half .. + 7 (zeros past the sequence).
   u32x4 qf[D / 16];
   auto load_q = [&](int qb) {
-    const int r = qb * kPpBlockM + wave * kRowsPerWave + (lane & 31);
+    const int r = qb * kBlockM + wave * kRowsPerWave + (lane & 31);
     const bool ok = r < a.seqlen_q;
     const uint16_t* src = qp + static_cast<int64_t>(ok ? r : 0) * a.q_ss + 8 * half;
 #pragma unroll
@@ -142,16 +144,16 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   // period and the epilogue. Measured per wave, loading them in the block's own prologue waited
   // 4,000-6,800 cycles (the second group's loads queue behind the first's).
   bool q_loaded = false;
-  // One query block of kPpBlockM rows: its own tile range, pipeline and epilogue (and, when next_qb
+  // One query block of kBlockM rows: its own tile range, pipeline and epilogue (and, when next_qb
   // >= 0, the query rows of block next_qb). Every wave has finished with the LDS ring and every
   // tile load has landed when it returns.
   auto process = [&](const int qb, const int next_qb) {
-    const int q0 = qb * kPpBlockM;
+    const int q0 = qb * kBlockM;
     const int row0 = q0 + wave * kRowsPerWave;
     const int my_row = row0 + (lane & 31);
 
     int kv_end = a.seqlen_k;
-    if (a.causal) kv_end = min(kv_end, min(q0 + kPpBlockM, a.seqlen_q) + a.causal_offset);
+    if (a.causal) kv_end = min(kv_end, min(q0 + kBlockM, a.seqlen_q) + a.causal_offset);
     const int num_tiles = kv_end > 0 ? (kv_end + kBlockN - 1) / kBlockN : 0;
     // Tiles this wave sees any key of (a prefix of the workgroup's tiles), and the first tile whose
     // scores need masking (it reaches past the sequence end or, causal, past the diagonal of the
@@ -437,13 +439,13 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
       constexpr int i = decltype(i_tag)::value;
       if (group == 0) {
         load_tile(i, i);
-      } else {
+      } else if (group == 1) {
         load_tile(i - 1, i + kStages - 1);
       }
     });
     if (group == 0) {
       wait_vmcnt<(kStages - 2) * kDmaPerWave>();
-    } else {
+    } else if (group == 1) {
       wait_vmcnt<(kStages - 3) * kDmaPerWave>();
     }
     phase_barrier();
@@ -468,6 +470,8 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     using kLoadsT = std::integral_constant<int, 3>;
     auto run = [&](auto group_tag) {
       constexpr int kGroup = decltype(group_tag)::value;
+      // Group 2 (head_dim 64) runs group 0's order and loads nothing.
+      constexpr bool kLoads = kGroup < 2;
       // Group 0 loads K(m + kStages - 1) into slot (m - 1) % kStages, group 1 V(m + kStages - 2)
       // into slot (m - 2) % kStages.
       constexpr int kLead = kGroup == 0 ? kStages - 1 : kStages - 2;
@@ -480,11 +484,11 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
         u32x4s w;
         auto hook = [&](auto i_tag) {
           constexpr int i = decltype(i_tag)::value;
-          if constexpr (i == 0) {
+          if constexpr (kLoads && i == 0) {
             w = tile_words_at(m + kLead, lead_tile);
             lead_tile += tile_bytes;
           }
-          if constexpr (i % 8 == 1 && i / 8 < kDmaPerWave) {
+          if constexpr (kLoads && i % 8 == 1 && i / 8 < kDmaPerWave) {
             issue_block(w, slot + kLead, std::integral_constant<int, i / 8>{});
           }
         };
@@ -495,13 +499,16 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
             mfma_phase(slot, std::bool_constant<kDoPv>{}, std::bool_constant<kDoQk>{}, hook);
           }
         };
-        if constexpr (kMode == kLastT::value) {
+        // (Not with three groups: there the tile loops' registers are tight enough that the
+        // compiler reuses registers these loads may still be writing, and then waits for every
+        // load in flight inside the loops. The next block loads its rows in its prologue.)
+        if constexpr (kMode == kLastT::value && kGroups == 2) {
           if (next_qb >= 0) {
             load_q(next_qb);
             q_loaded = true;
           }
         }
-        if constexpr (kGroup == 0) {
+        if constexpr (kGroup != 1) {
           if constexpr (kMode == kFirstT::value) prefetch_qk(slot);
           mfma();
           if constexpr (kDoQk) {
@@ -510,7 +517,7 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
             prefetch(slot + 1);
             softmax_phase(m);
           }
-          wait_vmcnt<kPendingK>();  // K(m + 1), first read in period m + 1
+          if constexpr (kLoads) wait_vmcnt<kPendingK>();  // K(m + 1), first read in period m + 1
           phase_barrier();
         } else {
           if constexpr (kMode == kFirstT::value) prefetch_qk(slot);
@@ -542,8 +549,10 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     };
     if (group == 0) {
       run(std::integral_constant<int, 0>{});
-    } else {
+    } else if (kGroups == 2 || group == 1) {
       run(std::integral_constant<int, 1>{});
+    } else {
+      if constexpr (kGroups == 3) run(std::integral_constant<int, 2>{});
     }
     // Loads past the end may still be in flight into free slots: each wave waits for its own here,
     // and the barrier below for the others', before the ring is reused.
@@ -562,7 +571,7 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
     constexpr int kChunks = D / 8;
     constexpr int kStageRow = 2 * D + 16;
     constexpr int kRowsPerStore = 64 / kChunks;
-    static_assert(kPpWaves * kRowsPerWave * kStageRow <= static_cast<int>(sizeof(smem)), "staging fits");
+    static_assert(kPpWavesOf<D> * kRowsPerWave * kStageRow <= static_cast<int>(sizeof(smem)), "staging fits");
     char* stage = reinterpret_cast<char*>(smem) + wave * kRowsPerWave * kStageRow;
     {
       char* wbase = stage + (lane & 31) * kStageRow + 8 * half;
@@ -607,16 +616,20 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
 
 template <typename Tag, int D>
 hipError_t launch_typed(PrefillArgs args, hipStream_t stream) {
-  args.q_blocks = (args.seqlen_q + kPpBlockM - 1) / kPpBlockM;
+  args.q_blocks = (args.seqlen_q + kPpBlockMOf<D> - 1) / kPpBlockMOf<D>;
   const int items_per_bh = args.causal ? (args.q_blocks + 1) / 2 : args.q_blocks;
   const int blocks = items_per_bh * args.batch * args.heads;
-  hipLaunchKernelGGL((prefill_pp_kernel<Tag, D>), dim3(blocks), dim3(kPpThreads), 0, stream, args);
+  hipLaunchKernelGGL((prefill_pp_kernel<Tag, D>), dim3(blocks), dim3(64 * kPpWavesOf<D>), 0, stream, args);
   return hipGetLastError();
 }
 
 }  // namespace
 }  // namespace pp
 }  // namespace prefill
+
+int prefill_pp_block_rows(int head_dim) {
+  return head_dim == 64 ? prefill::pp::kPpBlockMOf<64> : prefill::pp::kPpBlockMOf<128>;
+}
 
 hipError_t launch_prefill_pingpong(const PrefillArgs& args, DType dtype, int head_dim,
                                    hipStream_t stream) {

@@ -18,6 +18,15 @@ constexpr int kPpWaves = 8;
 constexpr int kPpThreads = 64 * kPpWaves;
 constexpr int kPpBlockM = kRowsPerWave * kPpWaves;  // 256 query rows per workgroup
 constexpr int kLoadWaves = 4;                       // waves per group: one group per tensor
+// Groups of four waves in the ping-pong kernel (prefill_pp.hip): two at head_dim 128, three at 64,
+// where a wave's softmax phase is much longer than its 16-MFMA phase and a third wave per SIMD
+// keeps the matrix pipe fed while two are in their softmax.
+template <int D>
+constexpr int kPpGroups = D == 64 ? 3 : 2;
+template <int D>
+constexpr int kPpWavesOf = 4 * kPpGroups<D>;
+template <int D>
+constexpr int kPpBlockMOf = kRowsPerWave * kPpWavesOf<D>;  // 256 rows at D = 128, 384 at 64
 constexpr int kXcds = 8;
 constexpr float kLn2 = 0.693147180559945309f;
 // Reference point of a row that has not seen a key yet: finite, so a masked score (-inf) still
