@@ -166,6 +166,9 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
       const int x = row0 + a.causal_offset - (kBlockN - 1);  // tile t needs masking iff 64 t > x
       mask_from = min(mask_from, x < 0 ? 0 : x / kBlockN + 1);
     }
+    // A wave whose rows all lie past the sequence (the last block of a ragged S_q) only keeps its
+    // turn in the loads and barriers.
+    if (row0 >= a.seqlen_q) my_tiles = 0;
 
     if (!q_loaded) {
       load_q(qb);
