@@ -195,6 +195,36 @@ def test_large_scores(impl, dtype, route):
     check_prefill(out, lse, q, k, v, causal=True)
 
 
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_dominant_key_after_the_first_tiles(dtype, head_dim, causal, route):
+    # Rows whose largest key arrives after their first 64-key tile and holds 15-75% of the row
+    # (its score 5 to 8 above the row's typical one): the kernels move their reference points to
+    # such keys (a point left below one keeps its probability far above 1 and rounded to the input
+    # type, an error that scales with the key's share). In a CPU emulation of the kernels'
+    # arithmetic on these inputs the moved point gives 0.3 of this rule's bound, a point that
+    # never moves after the first tile 0.5. Non-causal: row r < S - 64 gets key
+    # 64 + (37 r mod (S - 64)) (a bijection, so every planted key is its row's own); causal: row
+    # r >= 64 gets its own diagonal key, in its last tile, a masked one.
+    print(f"prefill dominant key {dtype} D={head_dim} causal={causal} route={route}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    batch, seqlen, heads = 2, 700, 4
+    q, k, v = (torch.randn(batch, seqlen, heads, head_dim, device="cuda", generator=gen)
+               for _ in range(3))
+    if causal:
+        rows = torch.arange(64, seqlen, device="cuda")
+        keys = rows
+    else:
+        rows = torch.arange(seqlen - 64, device="cuda")
+        keys = 64 + (rows * 37) % (seqlen - 64)
+    share = torch.linspace(5.0, 8.0, len(rows), device="cuda")[None, :, None, None]
+    k[:, keys] = q[:, rows] / q[:, rows].norm(dim=-1, keepdim=True) * share
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    out, lse = flash_lab.attention(q, k, v, causal=causal, return_lse=True)
+    check_prefill(out, lse, q, k, v, causal)
+
+
 @pytest.mark.parametrize("head_dim", [64, 128])
 @pytest.mark.parametrize("impl,dtype", IMPLS, ids=lambda x: str(x).replace("torch.", ""))
 def test_strided_inputs(impl, dtype, head_dim, route):
