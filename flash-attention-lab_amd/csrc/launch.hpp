@@ -91,7 +91,8 @@ hipError_t launch_prefill(const PrefillArgs& args, DType dtype, int head_dim, hi
 hipError_t launch_prefill_pingpong(const PrefillArgs& args, DType dtype, int head_dim,
                                    hipStream_t stream);
 // The same kernel for causal calls with a pair of query blocks per workgroup run as one stream of
-// key tiles (prefill_causal.hip); launch_prefill_pingpong routes causal calls to it.
+// key tiles (prefill_causal.hip); launch_prefill_pingpong routes causal calls to it when the
+// FL_KNOB_PREFILL_CAUSAL_STREAM knob is 1.
 // Query rows per workgroup of the ping-pong kernel at this head_dim.
 int prefill_pp_block_rows(int head_dim);
 hipError_t launch_prefill_causal_stream(const PrefillArgs& args, DType dtype, int head_dim,

@@ -365,26 +365,34 @@ static_assert(kPrefillBlockN == prefill::kBlockN, "host and kernel tile widths d
 #define FL_PREFILL_PINGPONG 1
 #endif
 
-// Below this many ping-pong workgroups (256 query rows each at head_dim 128, 384 at 64; causal
-// blocks paired; one per CU) a problem runs on this kernel instead, whose 128-row workgroups (two per CU) spread a
-// short prompt over more CUs. Measured on MI355X at B=1, H=32, causal: S=1024 takes 24.6 us here
-// against 42.7 us on the ping-pong kernel (64 workgroups), S=2048 ties, S=4096 (256 ping-pong
-// workgroups) is 128 us there against 161 us here. The FL_KNOB_PREFILL_PP_MIN_WG knob overrides it
-// (so tests can route one shape to either kernel).
-int prefill_pp_min_workgroups() {
+// Which prefill kernel a call runs. Below 256 ping-pong workgroups non-causal, 128 causal (256 query
+// rows each at head_dim 128, 384 at 64; causal blocks paired; one workgroup per CU), this kernel,
+// whose 128-row workgroups (two per CU) spread a short prompt over more CUs. Measured on MI355X
+// (TFLOP/s, ping-pong / this kernel, B=1, H=32, D = 128): S=1024 non-causal (128 workgroups)
+// 532 / 552, S=2048 (256) 1,083 / 957; causal S=1024 (64) 242 / 261, S=2048 (128) 642 / 551; B=4
+// causal S=512 (128) 270 / 269. Also this kernel: a non-causal call whose ping-pong blocks would be
+// more than a quarter padding (at head_dim 64, S = 512 pads 256 of 768 rows) and that needs more
+// than one round of workgroups, where the padded blocks take a round's time for a third of its
+// rows: H=32, D = 64, S = 512, B=16 523 / 618, B=32 537 / 654; one round (B=4) 276 / 230; 11%
+// padding (S = 2048, B=8, H=16) 931 / 819. The FL_KNOB_PREFILL_PP_MIN_WG knob replaces all of
+// this with its own workgroup threshold (so tests can route one shape to either kernel).
+bool prefill_on_pingpong(const PrefillArgs& args, int head_dim) {
+  const int rows = prefill_pp_block_rows(head_dim);
+  const int64_t pp_blocks = (args.seqlen_q + rows - 1) / rows;
+  const int64_t pp_items = args.causal ? (pp_blocks + 1) / 2 : pp_blocks;
+  const int64_t workgroups = pp_items * args.batch * args.heads;
   const int v = knob(FL_KNOB_PREFILL_PP_MIN_WG);
-  return v >= 0 ? v : 256;
+  if (v >= 0) return workgroups >= v;
+  if (args.causal) return workgroups >= 128;
+  const int64_t padding = pp_blocks * rows - args.seqlen_q;
+  if (4 * padding > pp_blocks * rows && workgroups > 256) return false;
+  return workgroups >= 256;
 }
 
 hipError_t launch_prefill(const PrefillArgs& args, DType dtype, int head_dim, hipStream_t stream) {
   using namespace prefill;
-  if (FL_PREFILL_PINGPONG) {
-    const int rows = prefill_pp_block_rows(head_dim);
-    const int64_t pp_blocks = (args.seqlen_q + rows - 1) / rows;
-    const int64_t pp_items = args.causal ? (pp_blocks + 1) / 2 : pp_blocks;
-    if (pp_items * args.batch * args.heads >= prefill_pp_min_workgroups())
-      return launch_prefill_pingpong(args, dtype, head_dim, stream);
-  }
+  if (FL_PREFILL_PINGPONG && prefill_on_pingpong(args, head_dim))
+    return launch_prefill_pingpong(args, dtype, head_dim, stream);
   if (dtype == DType::bf16) {
     return head_dim == 64 ? launch_typed<bf16_tag, 64>(args, stream)
                           : launch_typed<bf16_tag, 128>(args, stream);

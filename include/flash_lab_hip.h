@@ -173,8 +173,9 @@ int fl_mfma_tile_test(const void* a, const void* b, float* c, int32_t k, int32_t
  * in flight. value -1 restores the built-in rule; fl_set_knob rejects an
  * unknown knob or a value outside the knob's range with FL_ERR_INVALID.
  *   FL_KNOB_PREFILL_PP_MIN_WG      [0, 2^30]: fewest ping-pong workgroups
- *                                  for which prefill runs the 8-wave kernel
- *                                  (default 256; 0 = always, 2^30 = never).
+ *                                  for which prefill runs the ping-pong
+ *                                  kernel (default 256 non-causal, 128
+ *                                  causal; 0 = always, 2^30 = never).
  *   FL_KNOB_DECODE_MFMA_MIN_GROUP  [1, 2^20]: smallest GQA group the
  *                                  matrix-core decode kernel takes (default
  *                                  4 at head_dim 128 and 64; above 32 =
