@@ -283,6 +283,7 @@ def time_op(run, steps: int, warmup: int, flush=None, label: str = "step") -> tu
 
 
 CLOCK_WINDOW_S = 1.0  # the GPU clock and power are sampled over this much of the same work
+PREROLL_S = 1.0  # after this much of it, unsampled
 
 
 def gpu_window(run, step_ms: float, flush=None, seconds: float = CLOCK_WINDOW_S) -> dict:
@@ -298,30 +299,39 @@ def gpu_window(run, step_ms: float, flush=None, seconds: float = CLOCK_WINDOW_S)
     from flash_lab.observe import ClockSampler
 
     per_batch = max(1, int(25.0 / max(step_ms, 1e-3)))
+    queued = []
+
+    def batch():
+        for _ in range(per_batch):
+            if flush is not None:
+                flush.zero_()
+            run()
+        event = torch.cuda.Event()
+        event.record()
+        queued.append(event)
+        if len(queued) > 2:
+            queued.pop(0).synchronize()
+
     with ClockSampler(interval_ms=0) as sampler:
         if not sampler.available:
             return {"available": False, "reason": "amdsmi cannot read this GPU"}
-        torch.cuda.synchronize()
+        # The board's metrics lag the load (readings from an idle spell a fraction of a second
+        # earlier, e.g. the host-side check before the timing), so the same work runs PREROLL_S
+        # before the sampled window.
         start = time.time()
-        queued = []
+        while time.time() - start < PREROLL_S:
+            batch()
+        start = time.time()
         steps = 0
         while time.time() - start < seconds:
-            for _ in range(per_batch):
-                if flush is not None:
-                    flush.zero_()
-                run()
+            batch()
             steps += per_batch
-            event = torch.cuda.Event()
-            event.record()
-            queued.append(event)
-            if len(queued) > 2:
-                queued.pop(0).synchronize()
             sampler.sample()
         torch.cuda.synchronize()
         end = time.time()
         window = sampler.window(start, end)
-    return {"available": window is not None, "window_s": end - start, "steps": steps,
-            **(window or {})}
+    return {"available": window is not None, "window_s": end - start, "preroll_s": PREROLL_S,
+            "steps": steps, **(window or {})}
 
 
 # ----------------------------------------------------------------------------------------------
