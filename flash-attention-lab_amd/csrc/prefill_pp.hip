@@ -15,12 +15,14 @@
 // softmax wave's phase costs about 5 cycles per instruction (about 9.6 per exponential) and must
 // stay below the MFMA phase's 1024 cycles: everything that is not softmax arithmetic (tile loads,
 // their descriptors) is issued by the MFMA wave, which has idle issue slots while its MFMAs run.
-// At head_dim 64 the MFMA phase is 16 MFMAs (512 cycles) and the softmax phase, the same as at
-// 128, sets the half-period; the kernel still beats the 4-wave kernel of prefill_fwd.hip there.
+// At head_dim 64 the MFMA phase is 16 MFMAs (512 cycles) against the same softmax as at 128, and
+// a wave runs the two back to back in each period, so two waves per SIMD leave the matrix pipe
+// idle most of the time: there the workgroup has a third group of four waves (168 VGPRs each, three
+// waves per SIMD), which runs group 0's order and loads nothing.
 //
-//  * Workgroup: 8 waves x 32 query rows = 256 rows of one (batch, head). Waves w and w + 4 share a
-//    SIMD (the dispatcher deals waves to SIMDs with period 4). Group 0 is waves 0-3, group 1 waves
-//    4-7: one wave of each group per SIMD.
+//  * Workgroup: 8 waves x 32 query rows = 256 rows of one (batch, head) at head_dim 128, 12 waves
+//    (384 rows) at 64. Waves w, w + 4 (and w + 8) share a SIMD (the dispatcher deals waves to
+//    SIMDs with period 4). Group g is waves 4g .. 4g + 3: one wave of each group per SIMD.
 //  * Time is cut into periods by workgroup barriers, one per tile. In the first half of period m
 //    group 0 runs MFMA(m) = P V of tile m-1 then S = K Q^T of tile m (32 MFMAs) while group 1 runs
 //    the softmax of tile m-1; in the second half the roles swap. Nothing holds the groups to the
