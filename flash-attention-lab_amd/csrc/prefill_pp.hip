@@ -235,7 +235,9 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
     constexpr int kPv = 4 * (D / 32);  // P V MFMAs: key step kk = i / (D / 32), dim block nb
     constexpr int kQk = 2 * (D / 16);  // K Q^T MFMAs: dim step ks = j / 2, key block j % 2
     constexpr int kSteps = kPv + kQk;
-    constexpr int kAhead = FL_PP_AHEAD;
+    // (One at head_dim 64: at three waves per SIMD a second one spills two registers, outside the
+    // tile loops, for the same speed.)
+    constexpr int kAhead = D == 64 ? 1 : FL_PP_AHEAD;
     constexpr int kLeadPv = kPv - 4;
     constexpr int kTail = kPv - kLeadPv;  // P V steps after K Q^T
     static_assert(kAhead >= 1 && kAhead <= kLeadPv, "prefetched fragments are V fragments");
