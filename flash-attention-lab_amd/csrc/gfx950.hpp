@@ -7,6 +7,9 @@
 //   v_mfma_f32_32x32x16_{bf16,f16}: A[m][k] in lane m + 32 * (k / 8), element k % 8;
 //     B[k][n] in lane n + 32 * (k / 8), element k % 8; D[m][n] in lane n + 32 * ((m / 4) % 2),
 //     register 4 * (m / 8) + m % 4.
+//   v_mfma_f32_16x16x32_{bf16,f16}: A[m][k] in lane m + 16 * (k / 8), element k % 8;
+//     B[k][n] in lane n + 16 * (k / 8), element k % 8; D[m][n] in lane n + 16 * (m / 4),
+//     register m % 4.
 //   ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives as element e the
 //     16-bit value i % 4 of the 8 bytes addressed by lane 4 * e + i / 4 of the same group.
 #pragma once
@@ -56,6 +59,11 @@ struct Elem<bf16_tag> {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
+  static __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static constexpr uint32_t kOnePair = 0x3F803F80u;  // {1.0, 1.0}
 };
 
 template <>
@@ -75,6 +83,11 @@ struct Elem<f16_tag> {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
+  static __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static constexpr uint32_t kOnePair = 0x3C003C00u;  // {1.0, 1.0}
 };
 
 template <>

@@ -18,7 +18,9 @@
 // At head_dim 64 the MFMA phase is 16 MFMAs (512 cycles) against the same softmax as at 128, and
 // a wave runs the two back to back in each period, so two waves per SIMD leave the matrix pipe
 // idle most of the time: there the workgroup has a third group of four waves (168 VGPRs each, three
-// waves per SIMD), which runs group 0's order and loads nothing.
+// waves per SIMD), which runs group 1's order and loads nothing. The VALU then bounds the period
+// (one wave's softmax at a time keeps it busy; 32 of its ~90 instructions are exponentials), so at
+// 64 the row sums are taken by the matrix cores and issue priorities order the three softmaxes.
 //
 //  * Workgroup: 8 waves x 32 query rows = 256 rows of one (batch, head) at head_dim 128, 12 waves
 //    (384 rows) at 64. Waves w, w + 4 (and w + 8) share a SIMD (the dispatcher deals waves to
@@ -74,6 +76,19 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int group = wave >> 2;
   const int half = lane >> 5;
+
+  // Row sums on the matrix cores, at head_dim 64 only: there the softmax's VALU work bounds the
+  // kernel and the matrix pipe has room. For key step kk, P^T's fragment pf[kk] (the 32x32x16 B
+  // operand: lane l holds 8 of the step's keys of row l % 32) is also the B operand of one
+  // v_mfma_f32_16x16x32, which reads it as B[k][n] in lane n + 16 (k / 8): lane group g = l / 16
+  // holds row n + 16 (g % 2), half g / 2 of the step's keys. The A operand is a 0/1 selector,
+  // A[m][k] = 1 iff (k / 8) % 2 == (m / 4) % 2, so D[m][n] is the step's sum of row
+  // n + 16 ((m / 4) % 2), which lands in lane n + 16 (m / 4): every register of lane l holds the
+  // sum of its own row l % 32 over both halves. Lane l holds A[l % 16][8 (l / 16) + e], e = 0..7,
+  // all equal. This sums the probabilities as rounded for P V, so o and l agree exactly on them.
+  constexpr bool kMfmaSums = D == 64;
+  const uint32_t sel_word = ((lane >> 4) & 1) == ((lane >> 2) & 1) ? E::kOnePair : 0u;
+  const u32x4 sum_sel{sel_word, sel_word, sel_word, sel_word};
 
   // Work item: (batch, head) and query blocks. Non-causal: one block per workgroup. Causal: the
   // blocks of a (batch, head) go in pairs (q_blocks - 1 - i, i), heavy first, so every workgroup
@@ -212,7 +227,8 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
     f32x16 s1 = f32x16{};
     u32x4 pf[4] = {};
     float ref = kNoRef;
-    float l = 0.f;
+    float l = 0.f;  // the lane's part of its row's sum; with kMfmaSums, the whole row's
+    f32x4 ls = {};  // kMfmaSums: P's row sums from the last MFMA phase, added by the next softmax
     const float sl2 = a.scale_log2;
     const int last_key = a.causal ? min(a.seqlen_k - 1, my_row + a.causal_offset) : a.seqlen_k - 1;
 
@@ -235,9 +251,9 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
     constexpr int kPv = 4 * (D / 32);  // P V MFMAs: key step kk = i / (D / 32), dim block nb
     constexpr int kQk = 2 * (D / 16);  // K Q^T MFMAs: dim step ks = j / 2, key block j % 2
     constexpr int kSteps = kPv + kQk;
-    // (One at head_dim 64: at three waves per SIMD a second one spills two registers, outside the
-    // tile loops, for the same speed.)
-    constexpr int kAhead = D == 64 ? 1 : FL_PP_AHEAD;
+    // (At head_dim 64 with one fragment ahead every MFMA waited for its LDS read: a phase took
+    // ~1,200 cycles for 576 cycles of MFMAs, against ~650 with two.)
+    constexpr int kAhead = FL_PP_AHEAD;
     constexpr int kLeadPv = kPv - 4;
     constexpr int kTail = kPv - kLeadPv;  // P V steps after K Q^T
     static_assert(kAhead >= 1 && kAhead <= kLeadPv, "prefetched fragments are V fragments");
@@ -304,7 +320,15 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
       }
     };
     constexpr int kMaxOps = 18;
-    auto mfma_phase = [&](int slot, auto pv_tag, auto qk_tag, auto&& hook) {
+    // Issue priorities (s_setprio): a wave in its MFMA phase outranks the others, so its MFMAs issue
+    // as soon as their operands are ready. With three groups the softmax phases are ranked too,
+    // group 1 over group 2 over group 0: one softmax at a time keeps the VALU busy (each is ~90
+    // instructions, 32 of them exponentials, and a second wave's softmax only fills its gaps), and
+    // waves of equal priority are served oldest first, which would put group 0's first. In this
+    // order group 0's MFMA phase runs during group 1's softmax, group 1's during group 2's, and
+    // group 2's during group 0's, which ends the period.
+    constexpr int kMfmaPrio = kGroups == 3 ? 3 : 1;
+    auto mfma_phase = [&](int slot, auto pv_tag, auto qk_tag, auto&& hook, auto prio_tag) {
       constexpr bool kDoPv = decltype(pv_tag)::value;
       constexpr bool kDoQk = decltype(qk_tag)::value;
       constexpr bool kFull = kDoPv && kDoQk;
@@ -321,6 +345,9 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
         if constexpr (i < kPv) {
           constexpr int kk = i / (D / 32), nb = i % (D / 32);
           o[nb] = E::mfma32(f, pf[kk], o[nb]);
+          if constexpr (kMfmaSums && nb == D / 32 - 1) {
+            ls = E::mfma16(sum_sel, pf[kk], kk == 0 ? f32x4{} : ls);
+          }
         } else {
           constexpr int j = i - kPv, ks = j / 2, blk = j % 2;
           f32x16& acc = blk == 0 ? s0 : s1;
@@ -328,7 +355,7 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
         }
       };
 #if FL_PP_SETPRIO == 1
-      __builtin_amdgcn_s_setprio(1);
+      __builtin_amdgcn_s_setprio(kMfmaPrio);
 #endif
       __builtin_amdgcn_sched_barrier(0);
       static_for<0, kSteps>([&](auto n_tag) {
@@ -348,7 +375,7 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
         __builtin_amdgcn_sched_barrier(0);
       });
 #if FL_PP_SETPRIO == 1
-      __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_s_setprio(decltype(prio_tag)::value);
 #endif
       // A K Q^T-only phase (tile 0) has no P V MFMAs to hide the tree behind.
       if constexpr (kDoQk && !kDoPv) static_for<0, kMaxOps>([&](auto op) { max_op(op); });
@@ -362,13 +389,20 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
     // P(t) from S(t) against the reference point: p = 2^(s scale_log2 + neg_shift), packed (rounded
     // to the input type) as the P V operand; returns the lane's sum of the unrounded probabilities
     // (fp32 adds: v_dot2 on the packed values would be shorter, but on gfx950 it waits behind the
-    // other wave's MFMAs, which more than doubles the phase).
+    // other wave's MFMAs, which more than doubles the phase), or 0 where the MFMA phase sums them.
     auto probabilities = [&](float neg_shift) -> float {
       f32x16 p0, p1;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         p0[j] = exp2_fast(fmaf(s0[j], sl2, neg_shift));
         p1[j] = exp2_fast(fmaf(s1[j], sl2, neg_shift));
+      }
+      if constexpr (kMfmaSums) {
+        pf[0] = p_frag<Tag, 0>(p0);
+        pf[1] = p_frag<Tag, 1>(p0);
+        pf[2] = p_frag<Tag, 0>(p1);
+        pf[3] = p_frag<Tag, 1>(p1);
+        return 0.f;
       }
       float r0 = p0[0];  // (not 0 + p: the compiler keeps that add, for -0)
       float r1 = p1[0];
@@ -392,6 +426,7 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
     // It runs only for tiles t < my_tiles: a wave's periods past its last visible tile are
     // loads-only.
     auto softmax_body = [&](int t) {
+      if constexpr (kMfmaSums) l += ls[0];  // P(t - 1)'s sums, relative to the current point
       float mx = tile_mx;
       if (t >= mask_from) {
         asm volatile("" ::: "memory");
@@ -420,7 +455,11 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
         for (int nb = 0; nb < D / 32; ++nb) o[nb] *= alpha;
         l *= alpha;
       }
-      l += probabilities(-ref);
+      if constexpr (kMfmaSums) {
+        probabilities(-ref);
+      } else {
+        l += probabilities(-ref);
+      }
     };
     auto softmax_phase = [&](int t) {
 #if FL_PP_SETPRIO == 2
@@ -477,8 +516,11 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
     using kLoadsT = std::integral_constant<int, 3>;
     auto run = [&](auto group_tag) {
       constexpr int kGroup = decltype(group_tag)::value;
-      // Group 2 (head_dim 64) runs group 0's order and loads nothing.
+      // Group 2 (head_dim 64) runs group 1's order and loads nothing.
       constexpr bool kLoads = kGroup < 2;
+      constexpr int kBasePrio =
+          kGroups == 3 && FL_PP_SETPRIO == 1 ? (kGroup == 1 ? 2 : kGroup == 2 ? 1 : 0) : 0;
+      using kPrioT = std::integral_constant<int, kBasePrio>;
       // Group 0 loads K(m + kStages - 1) into slot (m - 1) % kStages, group 1 V(m + kStages - 2)
       // into slot (m - 2) % kStages.
       constexpr int kLead = kGroup == 0 ? kStages - 1 : kStages - 2;
@@ -503,7 +545,7 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
           if constexpr (kMode == kLoadsT::value) {
             loads_only(hook);
           } else {
-            mfma_phase(slot, std::bool_constant<kDoPv>{}, std::bool_constant<kDoQk>{}, hook);
+            mfma_phase(slot, std::bool_constant<kDoPv>{}, std::bool_constant<kDoQk>{}, hook, kPrioT{});
           }
         };
         // (Not with three groups: there the tile loops' registers are tight enough that the
@@ -515,7 +557,7 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
             q_loaded = true;
           }
         }
-        if constexpr (kGroup != 1) {
+        if constexpr (kGroup == 0) {
           if constexpr (kMode == kFirstT::value) prefetch_qk(slot);
           mfma();
           if constexpr (kDoQk) {
@@ -533,11 +575,12 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
             softmax_phase(m - 1);
           }
           mfma();
-          wait_vmcnt<kPendingV>();  // V(m + 1), first read in period m + 1
+          if constexpr (kLoads) wait_vmcnt<kPendingV>();  // V(m + 1), first read in period m + 1
           phase_barrier();
         }
       };
       if (num_tiles == 0) return;  // no key at all: nothing to multiply
+      if constexpr (kBasePrio != 0) __builtin_amdgcn_s_setprio(kBasePrio);
       int m = 0;
       if (wave_tiles > 0) {
         period(0, 0, kFirstT{});
@@ -553,6 +596,7 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
         ++m;
       }
       for (; m <= num_tiles; ++m) period(m, m % kStages, kLoadsT{});
+      if constexpr (kBasePrio != 0) __builtin_amdgcn_s_setprio(0);
     };
     if (group == 0) {
       run(std::integral_constant<int, 0>{});
@@ -566,22 +610,29 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
     wait_vmcnt<0>();
     if (q_loaded) consume_q();
 
-    const float lt = sum_halves(l);
+    const float lt = kMfmaSums ? l + ls[0] : sum_halves(l);
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     // Output rows go back whole, 16 bytes per lane (the accumulator layout would store 8 bytes per
     // lane into 32 rows a row stride apart): each wave stages its 32 rows in its own part of the
     // ring, rows padded by 16 bytes so that the row-per-lane writes spread over the banks, then
     // stores kRowsPerStore whole rows per instruction. Every staging address is one per-lane base
     // plus an immediate, so the addresses hold two registers (the bases are invariant across the
-    // blocks of a causal workgroup and would otherwise stay live through the tile loop).
+    // blocks of a causal workgroup and would otherwise stay live through the tile loop). With three
+    // groups the lane index they derive from goes through an empty asm here, so the compiler
+    // computes them here rather than before the tile loop (at 168 VGPRs, hoisted, they were
+    // spilled).
     phase_barrier();
+    int e_lane = lane;
+    if constexpr (kGroups == 3) asm volatile("" : "+v"(e_lane));
+    const int e_half = e_lane >> 5;
+    const int e_row = row0 + (e_lane & 31);
     constexpr int kChunks = D / 8;
     constexpr int kStageRow = 2 * D + 16;
     constexpr int kRowsPerStore = 64 / kChunks;
     static_assert(kPpWavesOf<D> * kRowsPerWave * kStageRow <= static_cast<int>(sizeof(smem)), "staging fits");
     char* stage = reinterpret_cast<char*>(smem) + wave * kRowsPerWave * kStageRow;
     {
-      char* wbase = stage + (lane & 31) * kStageRow + 8 * half;
+      char* wbase = stage + (e_lane & 31) * kStageRow + 8 * e_half;
 #pragma unroll
       for (int nb = 0; nb < D / 32; ++nb) {
 #pragma unroll
@@ -594,18 +645,18 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
       }
     }
     {
-      const int chunk = lane % kChunks;
-      const char* rbase = stage + (lane / kChunks) * kStageRow + 16 * chunk;
+      const int chunk = e_lane % kChunks;
+      const char* rbase = stage + (e_lane / kChunks) * kStageRow + 16 * chunk;
       uint16_t* obase = a.o + b * a.o_bs + h * a.o_hs + 8 * chunk;
 #pragma unroll
       for (int j = 0; j < kRowsPerWave / kRowsPerStore; ++j) {
-        const int r = row0 + j * kRowsPerStore + lane / kChunks;
+        const int r = row0 + j * kRowsPerStore + e_lane / kChunks;
         const u32x4 v = *reinterpret_cast<const u32x4*>(rbase + j * kRowsPerStore * kStageRow);
         if (r < a.seqlen_q) *reinterpret_cast<u32x4*>(obase + static_cast<int64_t>(r) * a.o_ss) = v;
       }
     }
-    if (my_row < a.seqlen_q && half == 0) {
-      a.lse[(static_cast<int64_t>(b) * a.heads + h) * a.seqlen_q + my_row] =
+    if (e_row < a.seqlen_q && e_half == 0) {
+      a.lse[(static_cast<int64_t>(b) * a.heads + h) * a.seqlen_q + e_row] =
           lt > 0.f ? ref * kLn2 + logf(lt) : -INFINITY;
     }
   };
