@@ -189,12 +189,16 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
-// Maxes the compiler turns into v_max_f32 / v_max3_f32. (Not inline assembly: an asm statement
+// Maxes the compiler turns into v_maximum3_f32, gfx950's NaN-propagating maximum (IEEE 754-2019
+// `maximum`). fmaxf's NaN-ignoring semantics cost a self-max (NaN quieting) on every operand the
+// compiler cannot prove quiet, such as a value read back from another lane; here a NaN can only
+// come from NaN inputs, which give a NaN output either way. (Not inline assembly: an asm statement
 // that reads an MFMA result is invisible to the compiler's wait-state insertion for the
-// MFMA -> VALU read hazard. Operands the compiler cannot prove quiet, e.g. masked selects, get a
-// self-max for IEEE-mode NaN quieting first; MFMA results need none.)
-__device__ __forceinline__ float max2_f32(float a, float b) { return fmaxf(a, b); }
-__device__ __forceinline__ float max3_f32(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+// MFMA -> VALU read hazard.)
+__device__ __forceinline__ float max2_f32(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float max3_f32(float a, float b, float c) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
 
 // max(x[l], x[l ^ 32]) and x[l] + x[l ^ 32] on every lane: one v_permlane32_swap (lanes 32-63 of
 // the first result and lanes 0-31 of the second are the other half's values).
