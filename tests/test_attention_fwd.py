@@ -40,6 +40,10 @@ SHAPES = [
     (2, 900, 1000, 8, 2, 128),
     (1, 481, 482, 4, 4, 64),
     (2, 355, 131, 4, 2, 128),
+    # Head_dim 64 (384-row blocks of three 4-wave groups): S_q > S_k over three blocks (causal rows
+    # without keys, groups without rows), and a last block whose 32 rows are one wave's.
+    (1, 900, 400, 4, 2, 64),
+    (2, 800, 1200, 8, 2, 64),
 ]
 SLOW_SHAPES = [(1, 4096, 4096, 4, 4, 128), (1, 8192, 8192, 2, 1, 64)]
 
