@@ -20,7 +20,7 @@ constexpr int kPpBlockM = kRowsPerWave * kPpWaves;  // 256 query rows per workgr
 constexpr int kLoadWaves = 4;                       // waves per group: one group per tensor
 // Groups of four waves in the ping-pong kernel (prefill_pp.hip): two at head_dim 128, three at 64,
 // where a wave's softmax phase is much longer than its 16-MFMA phase and a third wave per SIMD
-// keeps the matrix pipe fed while two are in their softmax.
+// keeps the matrix pipe fed while the others run their softmaxes.
 template <int D>
 constexpr int kPpGroups = D == 64 ? 3 : 2;
 template <int D>
