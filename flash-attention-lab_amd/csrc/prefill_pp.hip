@@ -496,8 +496,8 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
     }
     phase_barrier();
 
-    // Period m, one barrier at its end. Group 0: MFMA(m), softmax(m). Group 1: softmax(m - 1),
-    // then MFMA(m). Each MFMA phase issues its group's next tile between its MFMAs (the descriptor
+    // Period m, one barrier at its end. Group 0: MFMA(m), softmax(m). Group 1 (and group 2 at
+    // head_dim 64): softmax(m - 1), then MFMA(m). Each MFMA phase issues its group's next tile between its MFMAs (the descriptor
     // after MFMA 0, block j after MFMA 8j + 1). A group's periods run in four kinds:
     //  * first (m = 0): K Q^T only, as there is no tile -1 for a P V;
     //  * full, m = 1 .. G - 1, as a straight-line loop unrolled by kStages from slot 1 so that ring
@@ -518,6 +518,7 @@ __global__ void __launch_bounds__(64 * kPpWavesOf<D>)
       constexpr int kGroup = decltype(group_tag)::value;
       // Group 2 (head_dim 64) runs group 1's order and loads nothing.
       constexpr bool kLoads = kGroup < 2;
+      // The group's issue priority outside its MFMA phases, i.e. its softmax's (see kMfmaPrio).
       constexpr int kBasePrio =
           kGroups == 3 && FL_PP_SETPRIO == 1 ? (kGroup == 1 ? 2 : kGroup == 2 ? 1 : 0) : 0;
       using kPrioT = std::integral_constant<int, kBasePrio>;
