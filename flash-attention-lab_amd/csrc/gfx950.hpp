@@ -10,7 +10,8 @@
 //   v_mfma_f32_16x16x32_{bf16,f16}: A[m][k] in lane m + 16 * (k / 8), element k % 8;
 //     B[k][n] in lane n + 16 * (k / 8), element k % 8; D[m][n] in lane n + 16 * (m / 4),
 //     register m % 4. (Not covered by fl_mfma_tile_test: the head_dim 64 prefill takes every row
-//     sum with it, so the prefill parity tests at head_dim 64 pin it.)
+//     sum with it, so the prefill parity tests at head_dim 64 pin it; tests/test_row_sum_layout.py
+//     checks the row-sum selector against this layout on the CPU.)
 //   ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives as element e the
 //     16-bit value i % 4 of the 8 bytes addressed by lane 4 * e + i / 4 of the same group.
 #pragma once
